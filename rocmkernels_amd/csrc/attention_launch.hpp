@@ -1,0 +1,40 @@
+// Host-side launch interface between the C entry points (attention_abi.hip) and the kernels
+// (attention_forward.hip, attention_backward.hip). Arguments are already validated when these are called.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <rocmkernels_attention.h>
+
+namespace rk {
+
+struct ForwardArgs {
+    const float *q, *k, *v;
+    const bool *mask;
+    float *output, *lse;
+    int batch, heads, queries, keys, radius, causal;
+    rocmkernels_strides qs, ks, vs, os;
+};
+
+struct BackwardArgs {
+    const float *q, *k, *v;
+    const bool *mask;
+    const float *output, *lse, *upstream;
+    float *gradient_q, *gradient_k, *gradient_v, *delta;
+    int batch, heads, queries, keys, radius, causal;
+    rocmkernels_strides qs, ks, vs, os, us;
+};
+
+// Forward pass for head width D (32 or 64). statistics_only writes lse and skips V and the output.
+hipError_t launch_forward(int D, bool statistics_only, const ForwardArgs &a, hipStream_t stream);
+
+enum BackwardStage {
+    kBackwardAll = 0,    // delta, then dQ, then dK/dV
+    kBackwardDelta = 1,  // delta only
+    kBackwardQuery = 2,  // dQ only, reading delta
+    kBackwardKeyValue = 3, // dK/dV only, reading delta
+};
+
+hipError_t launch_backward(int D, BackwardStage stage, const BackwardArgs &a, hipStream_t stream);
+
+} // namespace rk
