@@ -63,7 +63,7 @@ class HipError(RuntimeError):
 
 
 def library_path():
-    return os.environ.get("ROCMKERNELS_LIBRARY", os.path.join(_HERE, "lib", LIBRARY_NAME))
+    return os.environ.get("ROCMKERNELS_LIBRARY") or os.path.join(_HERE, "lib", LIBRARY_NAME)
 
 
 def lib():

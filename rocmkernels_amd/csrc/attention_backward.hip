@@ -59,7 +59,7 @@ __global__ __launch_bounds__(kThreads) void attention_dq_kernel(const Tensor q, 
         dlt = 0.0f;
 #pragma unroll
         for (int c = 0; c < HALF; ++c) dlt = fmaf(dor[c], orow[c], dlt);
-        dlt += other_half(dlt);
+        dlt = halves_sum(dlt);
         if (wave == 0 && h == 0 && qvalid) delta[row] = dlt;
         if constexpr (MODE == kDeltaOnly) return;
     }
@@ -123,7 +123,7 @@ __global__ __launch_bounds__(kThreads) void attention_dq_kernel(const Tensor q, 
             float ds = p * (dp[v] - dlt);
             if (!full) {
                 const int r = tile_row(v, h);
-                const bool ok = ((bits >> r) & 1u) && in_window(s, query, key0 + r);
+                const bool ok = ((bits >> r) & 1u) && key0 + r >= window_lo(s, query) && key0 + r <= window_hi(s, query);
                 ds = ok ? ds : 0.0f;
             }
             sc[v] = ds;
@@ -277,7 +277,7 @@ __global__ __launch_bounds__(kThreads) void attention_dkdv_kernel(const Tensor q
             float ds = p * (dp[v] - dls[v]);
             if (!full) {
                 const int qq = q0 + tile_row(v, h);
-                const bool ok = visible && qq < s.queries && in_window(s, qq, key);
+                const bool ok = visible && qq < s.queries && qq >= window_query_lo(s, key) && qq <= window_query_hi(s, key);
                 p = ok ? p : 0.0f;
                 ds = ok ? ds : 0.0f;
             }
@@ -372,7 +372,9 @@ hipError_t run(const BackwardStage stage, const BackwardArgs &a, hipStream_t str
 hipError_t launch_backward(const int D, const BackwardStage stage, const BackwardArgs &a, hipStream_t stream) {
     const int64_t qblocks = static_cast<int64_t>((a.queries + kTile - 1) / kTile) * a.batch * a.heads;
     const int64_t kblocks = static_cast<int64_t>((a.keys + kTile - 1) / kTile) * a.batch * a.heads;
-    if (qblocks > 0x7fffffff || kblocks > 0x7fffffff) return hipErrorInvalidValue;
+    if (qblocks > 0x7fffffff || kblocks > 0x7fffffff || !sequence_fits(a.queries, a.qs, D) || !sequence_fits(a.keys, a.ks, D) ||
+            !sequence_fits(a.keys, a.vs, D) || !sequence_fits(a.queries, a.os, D) || !sequence_fits(a.queries, a.us, D))
+        return hipErrorInvalidValue;
     const bool vec = aligned16(a.q) && aligned16(a.k) && aligned16(a.v) && aligned16(a.output) && aligned16(a.upstream) &&
             aligned16(a.gradient_q) && aligned16(a.gradient_k) && aligned16(a.gradient_v) && strides4(a.qs) && strides4(a.ks) &&
             strides4(a.vs) && strides4(a.os) && strides4(a.us);

@@ -49,11 +49,75 @@ __device__ __forceinline__ f32x16 mfma(const float a, const float b, const f32x1
 
 __device__ __forceinline__ float exp2_fast(const float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Value of x held by the lane 32 positions away (the other half of the wave).
-__device__ __forceinline__ float other_half(const float x) { return __shfl_xor(x, 32); }
+// Combine x with the value held by the lane 32 positions away (the other half of the wave) using
+// v_permlane32_swap, a VALU op: no LDS round trip as with ds_bpermute.
+__device__ __forceinline__ float halves_max(const float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float halves_sum(const float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Bits lo..hi (inclusive, clamped to 0..31) set; 0 when the range is empty.
+__device__ __forceinline__ uint32_t bit_range(const int lo, const int hi) {
+    const int a = min(max(lo, 0), 32);
+    const int b = min(max(hi + 1, 0), 32);
+    return static_cast<uint32_t>(((1ull << b) - 1ull) & (~0ull << a));
+}
 
 __device__ __forceinline__ const float *sequence(const Tensor &t, const int b, const int head) {
     return t.data + (static_cast<int64_t>(b) * t.sb + static_cast<int64_t>(head) * t.sh);
+}
+
+// ---- buffer loads -----------------------------------------------------------------------------------------
+// Streamed tensors are read through buffer resources (one per sequence, in SGPRs): offsets are 32-bit, a
+// per-row SGPR offset replaces per-lane 64-bit address arithmetic, and the hardware range check returns 0 for
+// any access at or beyond `bytes`, so rows past the end of a sequence need no clamping and cannot fault.
+typedef __amdgpu_buffer_rsrc_t Buffer;
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+constexpr int kBufferWord3 = 0x00020000; // gfx9-family descriptor word 3: raw dword access
+
+__device__ __forceinline__ Buffer make_buffer(const void *base, const uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0), static_cast<int>(bytes), kBufferWord3);
+}
+
+// Byte extent of one sequence of a strided tensor: rows 0..rows-1 of `width` floats at `stride` floats.
+__device__ __forceinline__ uint32_t sequence_bytes(const int rows, const int stride, const int width) {
+    return static_cast<uint32_t>((static_cast<int64_t>(rows - 1) * stride + width) * 4);
+}
+
+__device__ __forceinline__ float buffer_load(const Buffer r, const uint32_t voffset, const uint32_t soffset) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(voffset), static_cast<int>(soffset), 0));
+}
+
+__device__ __forceinline__ f32x4 buffer_load4(const Buffer r, const uint32_t voffset, const uint32_t soffset) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(voffset), static_cast<int>(soffset), 0));
+}
+
+__device__ __forceinline__ int buffer_load_byte(const Buffer r, const uint32_t voffset) {
+    return __builtin_amdgcn_raw_buffer_load_b8(r, static_cast<int>(voffset), 0, 0);
+}
+
+// N contiguous floats at byte offset voffset (16-byte aligned when VEC).
+template<bool VEC, int N>
+__device__ __forceinline__ void buffer_load_span(float (&r)[N], const Buffer b, const uint32_t voffset) {
+    static_assert(N % 4 == 0);
+    if constexpr (VEC) {
+#pragma unroll
+        for (int i = 0; i < N / 4; ++i) {
+            const f32x4 x = buffer_load4(b, voffset + 16 * i, 0);
+            r[4 * i + 0] = x[0];
+            r[4 * i + 1] = x[1];
+            r[4 * i + 2] = x[2];
+            r[4 * i + 3] = x[3];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < N; ++i) r[i] = buffer_load(b, voffset + 4 * i, 0);
+    }
 }
 
 // N contiguous floats starting at p, or zeros when !ok. VEC uses 128-bit loads (p must be 16-byte aligned).
@@ -107,13 +171,21 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Visibility of (query, key) beyond the key mask: causal (key <= query) and local radius (|query - key| <= radius).
-__device__ __forceinline__ bool in_window(const Shape &s, const int query, const int key) {
-    bool ok = true;
-    if (s.causal) ok = ok && key <= query;
-    if (s.radius >= 0) ok = ok && abs(query - key) <= s.radius;
-    return ok;
+// Keys visible to `query` through the causal and radius windows form one interval [lo, hi].
+__device__ __forceinline__ int window_lo(const Shape &s, const int query) { return s.radius >= 0 ? query - s.radius : -0x40000000; }
+__device__ __forceinline__ int window_hi(const Shape &s, const int query) {
+    int hi = s.causal ? query : 0x40000000;
+    if (s.radius >= 0) hi = min(hi, query + s.radius);
+    return hi;
 }
+
+// Queries that see `key` through the causal and radius windows form one interval [lo, hi].
+__device__ __forceinline__ int window_query_lo(const Shape &s, const int key) {
+    int lo = s.causal ? key : -0x40000000;
+    if (s.radius >= 0) lo = max(lo, key - s.radius);
+    return lo;
+}
+__device__ __forceinline__ int window_query_hi(const Shape &s, const int key) { return s.radius >= 0 ? key + s.radius : 0x40000000; }
 
 // True when every (query, key) pair of the 32x32 tile at (q0, key0) is inside the causal/radius window.
 __device__ __forceinline__ bool tile_in_window(const Shape &s, const int q0, const int key0) {

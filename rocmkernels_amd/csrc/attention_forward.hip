@@ -52,81 +52,129 @@ __global__ __launch_bounds__(kThreads) void attention_forward_kernel(const Tenso
     }
     if (s.causal) last = min(last, q0 + kTile);
     const int ntiles = last > first ? (last - first + kTile - 1) / kTile : 0;
+    // This lane's query sees keys [wlo, whi] through the causal/radius window.
+    const int wlo = window_lo(s, query);
+    const int whi = window_hi(s, query);
+
+    const Buffer qbuf = make_buffer(sequence(q, b, head), sequence_bytes(s.queries, q.st, D));
+    const Buffer kbuf = make_buffer(sequence(k, b, head), sequence_bytes(s.keys, k.st, D));
+    const Buffer vbuf = make_buffer(sequence(v, b, head), sequence_bytes(s.keys, v.st, D));
+    const Buffer mbuf = make_buffer(mask + static_cast<int64_t>(b) * s.keys, static_cast<uint32_t>(s.keys));
+    const uint32_t kstep = 4u * k.st; // bytes between consecutive keys
+    const uint32_t vstep = 4u * v.st;
 
     float qr[HALF];
-    load_span<VEC>(qr, sequence(q, b, head) + static_cast<int64_t>(query) * q.st + h * HALF, query < s.queries);
+    buffer_load_span<VEC>(qr, qbuf, static_cast<uint32_t>(query) * (4u * q.st) + 4u * h * HALF); // rows >= queries read 0
 
-    const float *kbase = sequence(k, b, head);
-    const float *vbase = sequence(v, b, head);
-    const uint8_t *mrow = mask + static_cast<int64_t>(b) * s.keys;
-
+    // Online-softmax state of this lane's query over the tiles this wave visits. m_run is the raw maximum of
+    // q·k; mc_run = m_run·c2 rounded once, the exponent offset every p = exp2(s·c2 - mc) of the state uses, so
+    // that alpha = exp2(mc_old - mc_new) is exactly 1 when the maximum does not move.
     float m_run = -INFINITY;
+    float mc_run = -INFINITY;
     float l_run = 0.0f;
     f32x16 o[DT];
 #pragma unroll
     for (int t = 0; t < DT; ++t) o[t] = f32x16{};
 
-    for (int tile = wave; tile < ntiles; tile += kWaves) {
-        const int key0 = first + tile * kTile;
-        const int key = key0 + col;
-        const bool in_range = key < s.keys;
-        const bool visible = in_range && mrow[key] != 0;
-        const uint32_t bits = static_cast<uint32_t>(__ballot(visible));
-        if (bits == 0) continue; // every key of the tile is masked: contributes nothing
+    // K rows (Sᵀ A operand, row layout) and the mask byte of a tile are loaded one tile ahead; V (PV A operand,
+    // column layout) is loaded at the start of its own tile and lands while Sᵀ and the softmax run.
+    auto load_k = [&](float (&kr)[HALF], int &mb, const int key0) __attribute__((always_inline)) {
+        const uint32_t key = static_cast<uint32_t>(key0 + col);
+        mb = buffer_load_byte(mbuf, key); // keys >= s.keys read 0: masked
+        buffer_load_span<VEC>(kr, kbuf, key * kstep + 4u * h * HALF);
+    };
 
-        float kr[HALF];
-        load_span<VEC>(kr, kbase + static_cast<int64_t>(key) * k.st + h * HALF, in_range);
-        float vc[DT][16];
+    // prefetch() issues the next tile's K/mask loads. It runs after this tile's V loads and Sᵀ MFMAs are issued:
+    // vector-memory counters complete in order, so loads issued earlier than this tile's V would make the PV
+    // MFMAs wait for them.
+    auto step = [&](const float (&kr)[HALF], const int mb, const int key0, auto prefetch) __attribute__((always_inline)) {
+        const uint32_t bits = static_cast<uint32_t>(__ballot(mb != 0));
+        if (bits == 0) { // every key of the tile is masked: contributes nothing
+            prefetch();
+            return;
+        }
+
+        float vc[STATS ? 1 : DT][16];
         if constexpr (!STATS) {
+            const uint32_t vlane = static_cast<uint32_t>(key0 + 4 * h) * vstep + 4u * col;
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
-                const int r = tile_row(j, h);
-                const bool ok = (bits >> r) & 1u;
-                const float *vrow = vbase + static_cast<int64_t>(key0 + r) * v.st + col;
 #pragma unroll
-                for (int t = 0; t < DT; ++t) vc[t][j] = ok ? vrow[32 * t] : 0.0f;
+                for (int t = 0; t < DT; ++t) vc[t][j] = buffer_load(vbuf, vlane + 128u * t, static_cast<uint32_t>(8 * (j >> 2) + (j & 3)) * vstep);
             }
         }
 
         f32x16 sc{};
 #pragma unroll
         for (int c = 0; c < HALF; ++c) sc = mfma(kr[c], qr[c], sc);
+        __builtin_amdgcn_sched_barrier(0);
+        prefetch();
+        __builtin_amdgcn_sched_barrier(0);
 
-        const bool full = bits == 0xffffffffu && tile_in_window(s, q0, key0);
-        if (!full) {
+        if (bits != 0xffffffffu || !tile_in_window(s, q0, key0)) {
+            // Boundary tile: keep (query, key) pairs whose key is unmasked and inside this query's window.
+            const uint32_t visible = (bits & bit_range(wlo - key0, whi - key0)) >> (4 * h);
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int r = tile_row(v, h);
-                const bool ok = ((bits >> r) & 1u) && in_window(s, query, key0 + r);
-                sc[v] = ok ? sc[v] : -INFINITY;
+            for (int j = 0; j < 16; ++j) sc[j] = (visible >> (8 * (j >> 2) + (j & 3))) & 1u ? sc[j] : -INFINITY;
+            if constexpr (!STATS) {
+                if (bits != 0xffffffffu) {
+                    // Masked keys contribute exactly nothing, whatever their stored values hold.
+                    const uint32_t kept = bits >> (4 * h);
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) {
+#pragma unroll
+                        for (int t = 0; t < DT; ++t) vc[t][j] = (kept >> (8 * (j >> 2) + (j & 3))) & 1u ? vc[t][j] : 0.0f;
+                    }
+                }
             }
         }
 
         float mx = sc[0];
 #pragma unroll
-        for (int v = 1; v < 16; ++v) mx = fmaxf(mx, sc[v]);
-        mx = fmaxf(mx, other_half(mx));
+        for (int j = 1; j < 16; ++j) mx = fmaxf(mx, sc[j]);
+        mx = halves_max(mx);
         const float m_new = fmaxf(m_run, mx);
         const float mc = m_new == -INFINITY ? 0.0f : m_new * c2;
-        const float alpha = exp2_fast(fmaf(m_run, c2, -mc));
+        const float alpha = exp2_fast(mc_run - mc);
         float psum = 0.0f;
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            sc[v] = exp2_fast(fmaf(sc[v], c2, -mc));
-            psum += sc[v];
+        for (int j = 0; j < 16; ++j) {
+            sc[j] = exp2_fast(fmaf(sc[j], c2, -mc));
+            psum += sc[j];
         }
         l_run = fmaf(l_run, alpha, psum);
         m_run = m_new;
+        mc_run = m_new == -INFINITY ? -INFINITY : mc;
 
         if constexpr (!STATS) {
+            if (__ballot(alpha != 1.0f) != 0) {
 #pragma unroll
-            for (int t = 0; t < DT; ++t) o[t] *= alpha;
+                for (int t = 0; t < DT; ++t) o[t] *= alpha;
+            }
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
 #pragma unroll
                 for (int t = 0; t < DT; ++t) o[t] = mfma(vc[t][j], sc[j], o[t]);
             }
         }
+    };
+
+    float ka[HALF], kb[HALF];
+    int ma = 0, mb = 0;
+    int tile = wave;
+    if (tile < ntiles) load_k(ka, ma, first + tile * kTile);
+    while (tile < ntiles) {
+        int next = tile + kWaves;
+        step(ka, ma, first + tile * kTile, [&] {
+            if (next < ntiles) load_k(kb, mb, first + next * kTile);
+        });
+        tile = next;
+        if (tile >= ntiles) break;
+        next = tile + kWaves;
+        step(kb, mb, first + tile * kTile, [&] {
+            if (next < ntiles) load_k(ka, ma, first + next * kTile);
+        });
+        tile = next;
     }
 
     // Merge the per-wave states of the workgroup: waves 1..3 publish (m, l, Oᵀ) in LDS, wave 0 combines.
@@ -134,11 +182,11 @@ __global__ __launch_bounds__(kThreads) void attention_forward_kernel(const Tenso
     if (wave > 0) {
         partial[wave - 1][0][lane] = m_run;
         partial[wave - 1][1][lane] = l_run;
+        if constexpr (!STATS) {
 #pragma unroll
-        for (int t = 0; t < DT; ++t) {
+            for (int t = 0; t < DT; ++t) {
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                if constexpr (!STATS) partial[wave - 1][2 + 16 * t + v][lane] = o[t][v];
+                for (int j = 0; j < 16; ++j) partial[wave - 1][2 + 16 * t + j][lane] = o[t][j];
             }
         }
     }
@@ -148,8 +196,8 @@ __global__ __launch_bounds__(kThreads) void attention_forward_kernel(const Tenso
     float m_all = m_run;
 #pragma unroll
     for (int w = 0; w < kWaves - 1; ++w) m_all = fmaxf(m_all, partial[w][0][lane]);
-    const float mc = m_all == -INFINITY ? 0.0f : m_all * c2;
-    const float a0 = exp2_fast(fmaf(m_run, c2, -mc));
+    const float mc_all = m_all == -INFINITY ? 0.0f : m_all * c2;
+    const float a0 = exp2_fast(mc_run - mc_all);
     float l_all = l_run * a0;
     if constexpr (!STATS) {
 #pragma unroll
@@ -157,17 +205,18 @@ __global__ __launch_bounds__(kThreads) void attention_forward_kernel(const Tenso
     }
 #pragma unroll
     for (int w = 0; w < kWaves - 1; ++w) {
-        const float aw = exp2_fast(fmaf(partial[w][0][lane], c2, -mc));
+        const float mw = partial[w][0][lane];
+        const float aw = exp2_fast((mw == -INFINITY ? -INFINITY : mw * c2) - mc_all);
         l_all = fmaf(partial[w][1][lane], aw, l_all);
         if constexpr (!STATS) {
 #pragma unroll
             for (int t = 0; t < DT; ++t) {
 #pragma unroll
-                for (int v = 0; v < 16; ++v) o[t][v] = fmaf(partial[w][2 + 16 * t + v][lane], aw, o[t][v]);
+                for (int j = 0; j < 16; ++j) o[t][j] = fmaf(partial[w][2 + 16 * t + j][lane], aw, o[t][j]);
             }
         }
     }
-    l_all += other_half(l_all); // each half-wave summed the exponentials of its own 16 keys per tile
+    l_all = halves_sum(l_all); // each half-wave summed the exponentials of its own 16 keys per tile
 
     if (query >= s.queries) return;
     const bool nan_row = isnan(l_all);
@@ -223,7 +272,9 @@ void dispatch(const bool statistics_only, const ForwardArgs &a, const dim3 grid,
 
 hipError_t launch_forward(const int D, const bool statistics_only, const ForwardArgs &a, hipStream_t stream) {
     const int64_t tiles = static_cast<int64_t>((a.queries + kTile - 1) / kTile) * a.batch * a.heads;
-    if (tiles > 0x7fffffff) return hipErrorInvalidValue;
+    if (tiles > 0x7fffffff || !sequence_fits(a.queries, a.qs, D) || !sequence_fits(a.keys, a.ks, D) ||
+            (!statistics_only && !sequence_fits(a.keys, a.vs, D)))
+        return hipErrorInvalidValue;
     const dim3 grid(static_cast<unsigned>(tiles));
     if (D == 32) dispatch<32>(statistics_only, a, grid, stream);
     else dispatch<64>(statistics_only, a, grid, stream);

@@ -25,6 +25,13 @@ struct BackwardArgs {
     rocmkernels_strides qs, ks, vs, os, us;
 };
 
+// Buffer resources address one (batch, head) sequence with 32-bit byte offsets: every sequence of every
+// tensor must span less than 4 GiB ((rows - 1) * token stride + D floats).
+inline bool sequence_fits(const int rows, const rocmkernels_strides &s, const int width) {
+    const long long extent = (static_cast<long long>(rows) - 1) * s.token + width;
+    return s.token >= 0 && extent * 4 < (1ll << 32);
+}
+
 // Forward pass for head width D (32 or 64). statistics_only writes lse and skips V and the output.
 hipError_t launch_forward(int D, bool statistics_only, const ForwardArgs &a, hipStream_t stream);
 
