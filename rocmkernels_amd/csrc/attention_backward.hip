@@ -12,9 +12,10 @@
 //      B operand of the dQᵀ MFMAs directly.
 //   2. attention_dkdv_kernel (key-major): for its 32 keys streams the query tiles: S = Q·Kᵀ, dP = dO·Vᵀ,
 //      P and dS from lse/δ, dVᵀ += dOᵀ·P and dKᵀ += Qᵀ·dS, again feeding accumulators straight into MFMAs.
-// In both, the 4 waves of a workgroup split the streamed tiles and sum their partial gradients through LDS.
+// SPLIT waves share one 32-row item and split its streamed tiles; they sum their partial gradients through LDS.
 // Kernel 2 reads the δ that kernel 1 wrote; they are ordered by the stream, as in the reference
-// (Attention.hip:211-221).
+// (Attention.hip:211-221). Streamed operands are read through buffer resources (see attention_device.hpp), and
+// each tile's row-layout operands are loaded one tile ahead, after the current tile's MFMAs are issued.
 #include "attention_device.hpp"
 #include "attention_launch.hpp"
 
@@ -22,7 +23,7 @@ namespace rk {
 
 enum DqMode { kDqAndDelta = 0, kDeltaOnly = 1, kDqFromDelta = 2 };
 
-template<int D, int MODE, bool VEC>
+template<int D, int MODE, bool VEC, int SPLIT>
 __global__ __launch_bounds__(kThreads) void attention_dq_kernel(const Tensor q, const Tensor k, const Tensor v,
         const uint8_t *__restrict__ mask, const Tensor o, const float *__restrict__ lse, const Tensor du,
         float *__restrict__ dq, float *__restrict__ delta, const Shape s, const float scale) {
@@ -30,42 +31,41 @@ __global__ __launch_bounds__(kThreads) void attention_dq_kernel(const Tensor q, 
     constexpr int DT = D / 32;
 
     const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
     const int col = lane & 31;
     const int h = lane >> 5;
 
-    const int seqs = s.batch * s.heads;
     const int qtiles = (s.queries + kTile - 1) / kTile;
-    const int rank = blockIdx.x / seqs;
-    const int seq = blockIdx.x - rank * seqs;
-    const int qt = s.causal ? qtiles - 1 - rank : rank;
-    const int b = seq / s.heads;
-    const int head = seq - b * s.heads;
+    const WorkItem w = work_item<SPLIT>(s, qtiles);
+    const int qt = s.causal ? qtiles - 1 - w.rank : w.rank;
     const int q0 = qt * kTile;
     const int query = q0 + col;
-    const bool qvalid = query < s.queries;
-    const int64_t row = static_cast<int64_t>(seq) * s.queries + query;
+    const bool qvalid = w.valid && query < s.queries;
+    const int64_t row = static_cast<int64_t>(w.seq) * s.queries + query;
     const float c2 = scale * kLog2e;
 
+    const Buffer ubuf = make_buffer(sequence(du, w.b, w.head), sequence_bytes(s.queries, du.st, D));
+    const uint32_t qoff = static_cast<uint32_t>(query) * (4u * du.st) + 4u * h * HALF;
     float dor[HALF];
-    load_span<VEC>(dor, sequence(du, b, head) + static_cast<int64_t>(query) * du.st + h * HALF, qvalid);
+    buffer_load_span<VEC>(dor, ubuf, qvalid ? qoff : kNoRow);
 
     float dlt;
     if constexpr (MODE == kDqFromDelta) {
         dlt = qvalid ? delta[row] : 0.0f;
     } else {
+        const Buffer obuf = make_buffer(sequence(o, w.b, w.head), sequence_bytes(s.queries, o.st, D));
         float orow[HALF];
-        load_span<VEC>(orow, sequence(o, b, head) + static_cast<int64_t>(query) * o.st + h * HALF, qvalid);
+        buffer_load_span<VEC>(orow, obuf, qvalid ? static_cast<uint32_t>(query) * (4u * o.st) + 4u * h * HALF : kNoRow);
         dlt = 0.0f;
 #pragma unroll
         for (int c = 0; c < HALF; ++c) dlt = fmaf(dor[c], orow[c], dlt);
         dlt = halves_sum(dlt);
-        if (wave == 0 && h == 0 && qvalid) delta[row] = dlt;
+        if (w.sub == 0 && h == 0 && qvalid) delta[row] = dlt;
         if constexpr (MODE == kDeltaOnly) return;
     }
 
+    const Buffer qbuf = make_buffer(sequence(q, w.b, w.head), sequence_bytes(s.queries, q.st, D));
     float qr[HALF];
-    load_span<VEC>(qr, sequence(q, b, head) + static_cast<int64_t>(query) * q.st + h * HALF, qvalid);
+    buffer_load_span<VEC>(qr, qbuf, qvalid ? static_cast<uint32_t>(query) * (4u * q.st) + 4u * h * HALF : kNoRow);
     const float m = qvalid ? lse[2 * row] : -INFINITY;
     const float l = qvalid ? lse[2 * row + 1] : 0.0f;
     const bool row_ok = m != -INFINITY;
@@ -78,35 +78,42 @@ __global__ __launch_bounds__(kThreads) void attention_dq_kernel(const Tensor q, 
         last = min(last, q0 + kTile + s.radius);
     }
     if (s.causal) last = min(last, q0 + kTile);
-    const int ntiles = last > first ? (last - first + kTile - 1) / kTile : 0;
+    const int ntiles = (w.valid && last > first) ? (last - first + kTile - 1) / kTile : 0;
+    const int wlo = window_lo(s, query);
+    const int whi = window_hi(s, query);
 
-    const float *kbase = sequence(k, b, head);
-    const float *vbase = sequence(v, b, head);
-    const uint8_t *mrow = mask + static_cast<int64_t>(b) * s.keys;
+    const Buffer kbuf = make_buffer(sequence(k, w.b, w.head), sequence_bytes(s.keys, k.st, D));
+    const Buffer vbuf = make_buffer(sequence(v, w.b, w.head), sequence_bytes(s.keys, v.st, D));
+    const Buffer mbuf = make_buffer(mask + static_cast<int64_t>(w.b) * s.keys, static_cast<uint32_t>(s.keys));
+    const uint32_t kstep = 4u * k.st;
+    const uint32_t vstep = 4u * v.st;
 
     f32x16 acc[DT];
 #pragma unroll
     for (int t = 0; t < DT; ++t) acc[t] = f32x16{};
 
-    for (int tile = wave; tile < ntiles; tile += kWaves) {
-        const int key0 = first + tile * kTile;
-        const int key = key0 + col;
-        const bool in_range = key < s.keys;
-        const bool visible = in_range && mrow[key] != 0;
-        const uint32_t bits = static_cast<uint32_t>(__ballot(visible));
-        if (bits == 0) continue;
+    // K and V rows (Sᵀ and dPᵀ A operands) and the mask byte, one tile ahead.
+    auto load_rows = [&](float (&kr)[HALF], float (&vr)[HALF], int &mb, const int key0) __attribute__((always_inline)) {
+        const uint32_t key = static_cast<uint32_t>(key0 + col);
+        mb = buffer_load_byte(mbuf, key);
+        buffer_load_span<VEC>(kr, kbuf, key * kstep + 4u * h * HALF);
+        buffer_load_span<VEC>(vr, vbuf, key * vstep + 4u * h * HALF);
+    };
 
-        float kr[HALF], vr[HALF];
-        load_span<VEC>(kr, kbase + static_cast<int64_t>(key) * k.st + h * HALF, in_range);
-        load_span<VEC>(vr, vbase + static_cast<int64_t>(key) * v.st + h * HALF, in_range);
+    auto step = [&](const float (&kr)[HALF], const float (&vr)[HALF], const int mb, const int key0, auto prefetch)
+            __attribute__((always_inline)) {
+        const uint32_t bits = static_cast<uint32_t>(__ballot(mb != 0));
+        if (bits == 0) {
+            prefetch();
+            return;
+        }
+        // K in column layout (dQᵀ A operand): row key0 + tile_row(j, h), feature 32t + col.
         float kc[DT][16];
+        const uint32_t klane = static_cast<uint32_t>(key0 + 4 * h) * kstep + 4u * col;
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-            const int r = tile_row(j, h);
-            const bool ok = (bits >> r) & 1u;
-            const float *krow = kbase + static_cast<int64_t>(key0 + r) * k.st + col;
 #pragma unroll
-            for (int t = 0; t < DT; ++t) kc[t][j] = ok ? krow[32 * t] : 0.0f;
+            for (int t = 0; t < DT; ++t) kc[t][j] = buffer_load(kbuf, klane + 128u * t, static_cast<uint32_t>(8 * (j >> 2) + (j & 3)) * kstep);
         }
 
         f32x16 sc{}, dp{};
@@ -115,51 +122,61 @@ __global__ __launch_bounds__(kThreads) void attention_dq_kernel(const Tensor q, 
             sc = mfma(kr[c], qr[c], sc);
             dp = mfma(vr[c], dor[c], dp);
         }
+        __builtin_amdgcn_sched_barrier(0);
+        prefetch();
+        __builtin_amdgcn_sched_barrier(0);
 
-        const bool full = bits == 0xffffffffu && tile_in_window(s, q0, key0);
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const float p = exp2_fast(fmaf(sc[v], c2, -mc)) * il;
-            float ds = p * (dp[v] - dlt);
-            if (!full) {
-                const int r = tile_row(v, h);
-                const bool ok = ((bits >> r) & 1u) && key0 + r >= window_lo(s, query) && key0 + r <= window_hi(s, query);
-                ds = ok ? ds : 0.0f;
+        for (int j = 0; j < 16; ++j) {
+            const float p = exp2_fast(fmaf(sc[j], c2, -mc)) * il;
+            sc[j] = p * (dp[j] - dlt);
+        }
+        if (bits != 0xffffffffu || !tile_in_window(s, q0, key0)) {
+            const uint32_t visible = (bits & bit_range(wlo - key0, whi - key0)) >> (4 * h);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) sc[j] = (visible >> (8 * (j >> 2) + (j & 3))) & 1u ? sc[j] : 0.0f;
+            if (bits != 0xffffffffu) {
+                const uint32_t kept = bits >> (4 * h); // masked keys contribute nothing, whatever K holds there
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+#pragma unroll
+                    for (int t = 0; t < DT; ++t) kc[t][j] = (kept >> (8 * (j >> 2) + (j & 3))) & 1u ? kc[t][j] : 0.0f;
+                }
             }
-            sc[v] = ds;
         }
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
 #pragma unroll
             for (int t = 0; t < DT; ++t) acc[t] = mfma(kc[t][j], sc[j], acc[t]);
         }
+    };
+
+    float ka[HALF], va[HALF], kb[HALF], vb[HALF];
+    int ma = 0, mb = 0;
+    int tile = w.sub;
+    if (tile < ntiles) load_rows(ka, va, ma, first + tile * kTile);
+    while (tile < ntiles) {
+        int next = tile + SPLIT;
+        step(ka, va, ma, first + tile * kTile, [&] {
+            if (next < ntiles) load_rows(kb, vb, mb, first + next * kTile);
+        });
+        tile = next;
+        if (tile >= ntiles) break;
+        next = tile + SPLIT;
+        step(kb, vb, mb, first + tile * kTile, [&] {
+            if (next < ntiles) load_rows(ka, va, ma, first + next * kTile);
+        });
+        tile = next;
     }
 
-    __shared__ float partial[kWaves - 1][16 * DT][kWave];
-    if (wave > 0) {
-#pragma unroll
-        for (int t = 0; t < DT; ++t) {
-#pragma unroll
-            for (int v = 0; v < 16; ++v) partial[wave - 1][16 * t + v][lane] = acc[t][v];
-        }
-    }
-    __syncthreads();
-    if (wave != 0) return;
-#pragma unroll
-    for (int w = 0; w < kWaves - 1; ++w) {
-#pragma unroll
-        for (int t = 0; t < DT; ++t) {
-#pragma unroll
-            for (int v = 0; v < 16; ++v) acc[t][v] += partial[w][16 * t + v][lane];
-        }
-    }
-    if (!qvalid) return;
+    split_sum<SPLIT>(acc, w.sub);
+    if (w.sub != 0 || !qvalid) return;
     float *dst = dq + row * D;
 #pragma unroll
     for (int t = 0; t < DT; ++t) store_tile_row<VEC>(dst + 32 * t, acc[t], scale, h);
 }
 
-template<int D, bool VEC>
+template<int D, bool VEC, int SPLIT>
 __global__ __launch_bounds__(kThreads) void attention_dkdv_kernel(const Tensor q, const Tensor k, const Tensor v,
         const uint8_t *__restrict__ mask, const float *__restrict__ lse, const Tensor du, const float *__restrict__ delta,
         float *__restrict__ dk, float *__restrict__ dv, const Shape s, const float scale) {
@@ -167,25 +184,25 @@ __global__ __launch_bounds__(kThreads) void attention_dkdv_kernel(const Tensor q
     constexpr int DT = D / 32;
 
     const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave); // wave-uniform: keeps tile bookkeeping scalar
     const int col = lane & 31;
     const int h = lane >> 5;
 
-    const int seqs = s.batch * s.heads;
-    const int rank = blockIdx.x / seqs;
-    const int seq = blockIdx.x - rank * seqs;
-    const int b = seq / s.heads;
-    const int head = seq - b * s.heads;
-    const int key0 = rank * kTile; // under a causal mask the first key tiles see the most queries
+    const int ktiles = (s.keys + kTile - 1) / kTile;
+    const WorkItem w = work_item<SPLIT>(s, ktiles);
+    const int key0 = w.rank * kTile; // under a causal mask the first key tiles see the most queries
     const int key = key0 + col;
-    const bool in_range = key < s.keys;
-    const bool visible = in_range && mask[static_cast<int64_t>(b) * s.keys + key] != 0;
+    const bool in_range = w.valid && key < s.keys;
+    const Buffer mbuf = make_buffer(mask + static_cast<int64_t>(w.b) * s.keys, static_cast<uint32_t>(s.keys));
+    const bool visible = in_range && buffer_load_byte(mbuf, static_cast<uint32_t>(key)) != 0;
     const uint32_t bits = static_cast<uint32_t>(__ballot(visible));
     const float c2 = scale * kLog2e;
 
+    const Buffer kbuf = make_buffer(sequence(k, w.b, w.head), sequence_bytes(s.keys, k.st, D));
+    const Buffer vbuf = make_buffer(sequence(v, w.b, w.head), sequence_bytes(s.keys, v.st, D));
     float kr[HALF], vr[HALF];
-    load_span<VEC>(kr, sequence(k, b, head) + static_cast<int64_t>(key) * k.st + h * HALF, visible);
-    load_span<VEC>(vr, sequence(v, b, head) + static_cast<int64_t>(key) * v.st + h * HALF, visible);
+    buffer_load_span<VEC>(kr, kbuf, in_range ? static_cast<uint32_t>(key) * (4u * k.st) + 4u * h * HALF : kNoRow);
+    buffer_load_span<VEC>(vr, vbuf, in_range ? static_cast<uint32_t>(key) * (4u * v.st) + 4u * h * HALF : kNoRow);
 
     int first = s.causal ? key0 : 0;
     int last = s.queries;
@@ -195,10 +212,16 @@ __global__ __launch_bounds__(kThreads) void attention_dkdv_kernel(const Tensor q
     }
     first = max(first, 0);
     const int ntiles = (bits != 0 && last > first) ? (last - first + kTile - 1) / kTile : 0;
+    // Queries that see this lane's key: [qlo, qhi] (also capped at the last query).
+    const int qlo = window_query_lo(s, key);
+    const int qhi = min(window_query_hi(s, key), s.queries - 1);
 
-    const float *qbase = sequence(q, b, head);
-    const float *ubase = sequence(du, b, head);
-    const int64_t rows = static_cast<int64_t>(seq) * s.queries;
+    const Buffer qbuf = make_buffer(sequence(q, w.b, w.head), sequence_bytes(s.queries, q.st, D));
+    const Buffer ubuf = make_buffer(sequence(du, w.b, w.head), sequence_bytes(s.queries, du.st, D));
+    const Buffer lbuf = make_buffer(lse + static_cast<int64_t>(w.seq) * s.queries * 2, static_cast<uint32_t>(s.queries) * 8u);
+    const Buffer dbuf = make_buffer(delta + static_cast<int64_t>(w.seq) * s.queries, static_cast<uint32_t>(s.queries) * 4u);
+    const uint32_t qstep = 4u * q.st;
+    const uint32_t ustep = 4u * du.st;
 
     __shared__ __align__(16) float stats[kWaves][3][kTile];
 
@@ -209,80 +232,77 @@ __global__ __launch_bounds__(kThreads) void attention_dkdv_kernel(const Tensor q
         acc_v[t] = f32x16{};
     }
 
-    for (int tile = wave; tile < ntiles; tile += kWaves) {
-        const int q0 = first + tile * kTile;
+    // Q and dO rows (S and dP A operands) and the raw softmax statistics of query q0 + col, one tile ahead.
+    struct Rows {
+        float qr[HALF], ur[HALF];
+        float m, l, d;
+    };
+    auto load_rows = [&](Rows &r, const int q0) __attribute__((always_inline)) {
+        const uint32_t qq = static_cast<uint32_t>(q0 + col);
+        buffer_load_span<VEC>(r.qr, qbuf, qq * qstep + 4u * h * HALF);
+        buffer_load_span<VEC>(r.ur, ubuf, qq * ustep + 4u * h * HALF);
+        r.m = buffer_load(lbuf, qq * 8u, 0);
+        r.l = buffer_load(lbuf, qq * 8u + 4u, 0);
+        r.d = buffer_load(dbuf, qq * 4u, 0);
+    };
 
-        // Per-query softmax constants for the 32 queries of the tile, staged once in this wave's LDS slice and
-        // read back in accumulator order (lane needs queries tile_row(v, h), v = 0..15).
+    auto step = [&](const Rows &r, const int q0, auto prefetch) __attribute__((always_inline)) {
+        // Per-query constants for the 32 queries of the tile, staged in this wave's LDS slice and read back in
+        // accumulator order (lane needs queries q0 + tile_row(j, h)). Queries past the end get exp2(-inf) = 0.
         wave_lds_sync();
         if (h == 0) {
-            const int qq = q0 + col;
-            float mcv = INFINITY, ilv = 0.0f, dl = 0.0f;
-            if (qq < s.queries) {
-                const float m = lse[2 * (rows + qq)];
-                if (m != -INFINITY) {
-                    mcv = m * kLog2e;
-                    ilv = 1.0f / lse[2 * (rows + qq) + 1];
-                }
-                dl = delta[rows + qq];
-            }
-            stats[wave][0][col] = mcv;
-            stats[wave][1][col] = ilv;
-            stats[wave][2][col] = dl;
+            const bool ok = q0 + col < s.queries && r.m != -INFINITY;
+            stats[wave][0][col] = ok ? r.m * kLog2e : INFINITY;
+            stats[wave][1][col] = ok ? 1.0f / r.l : 0.0f;
+            stats[wave][2][col] = r.d;
         }
         wave_lds_sync();
-        float mcs[16], ils[16], dls[16];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const f32x4 a = *reinterpret_cast<const f32x4 *>(&stats[wave][0][8 * u + 4 * h]);
-            const f32x4 bb = *reinterpret_cast<const f32x4 *>(&stats[wave][1][8 * u + 4 * h]);
-            const f32x4 c = *reinterpret_cast<const f32x4 *>(&stats[wave][2][8 * u + 4 * h]);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                mcs[4 * u + i] = a[i];
-                ils[4 * u + i] = bb[i];
-                dls[4 * u + i] = c[i];
-            }
-        }
 
-        const int qrow = q0 + col;
-        float qr[HALF], dor[HALF];
-        load_span<VEC>(qr, qbase + static_cast<int64_t>(qrow) * q.st + h * HALF, qrow < s.queries);
-        load_span<VEC>(dor, ubase + static_cast<int64_t>(qrow) * du.st + h * HALF, qrow < s.queries);
+        // Q and dO in column layout (dKᵀ and dVᵀ A operands): row q0 + tile_row(j, h), feature 32t + col.
         float qc[DT][16], uc[DT][16];
+        const uint32_t qlane = static_cast<uint32_t>(q0 + 4 * h) * qstep + 4u * col;
+        const uint32_t ulane = static_cast<uint32_t>(q0 + 4 * h) * ustep + 4u * col;
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-            const int r = q0 + tile_row(j, h);
-            const bool ok = r < s.queries;
-            const float *qp = qbase + static_cast<int64_t>(r) * q.st + col;
-            const float *up = ubase + static_cast<int64_t>(r) * du.st + col;
+            const uint32_t r8 = static_cast<uint32_t>(8 * (j >> 2) + (j & 3));
 #pragma unroll
             for (int t = 0; t < DT; ++t) {
-                qc[t][j] = ok ? qp[32 * t] : 0.0f;
-                uc[t][j] = ok ? up[32 * t] : 0.0f;
+                uc[t][j] = buffer_load(ubuf, ulane + 128u * t, r8 * ustep);
+                qc[t][j] = buffer_load(qbuf, qlane + 128u * t, r8 * qstep);
             }
         }
 
         f32x16 sc{}, dp{};
 #pragma unroll
         for (int c = 0; c < HALF; ++c) {
-            sc = mfma(qr[c], kr[c], sc);
-            dp = mfma(dor[c], vr[c], dp);
+            sc = mfma(r.qr[c], kr[c], sc);
+            dp = mfma(r.ur[c], vr[c], dp);
         }
+        __builtin_amdgcn_sched_barrier(0);
+        prefetch();
+        __builtin_amdgcn_sched_barrier(0);
 
-        const bool full = bits == 0xffffffffu && q0 + kTile <= s.queries && tile_in_window(s, q0, key0);
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            float p = exp2_fast(fmaf(sc[v], c2, -mcs[v])) * ils[v];
-            float ds = p * (dp[v] - dls[v]);
-            if (!full) {
-                const int qq = q0 + tile_row(v, h);
-                const bool ok = visible && qq < s.queries && qq >= window_query_lo(s, key) && qq <= window_query_hi(s, key);
-                p = ok ? p : 0.0f;
-                ds = ok ? ds : 0.0f;
+        for (int u = 0; u < 4; ++u) {
+            const f32x4 mcs = *reinterpret_cast<const f32x4 *>(&stats[wave][0][8 * u + 4 * h]);
+            const f32x4 ils = *reinterpret_cast<const f32x4 *>(&stats[wave][1][8 * u + 4 * h]);
+            const f32x4 dls = *reinterpret_cast<const f32x4 *>(&stats[wave][2][8 * u + 4 * h]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int j = 4 * u + i;
+                const float p = exp2_fast(fmaf(sc[j], c2, -mcs[i])) * ils[i];
+                sc[j] = p;
+                dp[j] = p * (dp[j] - dls[i]);
             }
-            sc[v] = p;
-            dp[v] = ds;
+        }
+        if (bits != 0xffffffffu || q0 + kTile > s.queries || !tile_in_window(s, q0, key0)) {
+            const uint32_t keep = visible ? bit_range(qlo - q0, qhi - q0) >> (4 * h) : 0u;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const bool ok = (keep >> (8 * (j >> 2) + (j & 3))) & 1u;
+                sc[j] = ok ? sc[j] : 0.0f;
+                dp[j] = ok ? dp[j] : 0.0f;
+            }
         }
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
@@ -292,34 +312,29 @@ __global__ __launch_bounds__(kThreads) void attention_dkdv_kernel(const Tensor q
                 acc_k[t] = mfma(qc[t][j], dp[j], acc_k[t]);
             }
         }
+    };
+
+    Rows ra, rb;
+    int tile = w.sub;
+    if (tile < ntiles) load_rows(ra, first + tile * kTile);
+    while (tile < ntiles) {
+        int next = tile + SPLIT;
+        step(ra, first + tile * kTile, [&] {
+            if (next < ntiles) load_rows(rb, first + next * kTile);
+        });
+        tile = next;
+        if (tile >= ntiles) break;
+        next = tile + SPLIT;
+        step(rb, first + tile * kTile, [&] {
+            if (next < ntiles) load_rows(ra, first + next * kTile);
+        });
+        tile = next;
     }
 
-    __shared__ float partial[kWaves - 1][32 * DT][kWave];
-    if (wave > 0) {
-#pragma unroll
-        for (int t = 0; t < DT; ++t) {
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                partial[wave - 1][16 * t + v][lane] = acc_k[t][v];
-                partial[wave - 1][16 * DT + 16 * t + v][lane] = acc_v[t][v];
-            }
-        }
-    }
-    __syncthreads();
-    if (wave != 0) return;
-#pragma unroll
-    for (int w = 0; w < kWaves - 1; ++w) {
-#pragma unroll
-        for (int t = 0; t < DT; ++t) {
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                acc_k[t][v] += partial[w][16 * t + v][lane];
-                acc_v[t][v] += partial[w][16 * DT + 16 * t + v][lane];
-            }
-        }
-    }
-    if (!in_range) return;
-    const int64_t krow = (static_cast<int64_t>(seq) * s.keys + key) * D;
+    split_sum<SPLIT>(acc_k, w.sub);
+    split_sum<SPLIT>(acc_v, w.sub);
+    if (w.sub != 0 || !in_range) return;
+    const int64_t krow = (static_cast<int64_t>(w.seq) * s.keys + key) * D;
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
         store_tile_row<VEC>(dk + krow + 32 * t, acc_k[t], scale, h);
@@ -334,36 +349,55 @@ bool strides4(const rocmkernels_strides &s) { return ((s.batch | s.head | s.toke
 
 Tensor tensor(const float *p, const rocmkernels_strides &s) { return Tensor{p, s.batch, s.head, s.token}; }
 
-template<int D, int MODE, bool VEC>
+unsigned grid_for(const int64_t items, const int split) { return static_cast<unsigned>((items + kWaves / split - 1) / (kWaves / split)); }
+
+template<int D, int MODE, bool VEC, int SPLIT>
 void launch_dq(const BackwardArgs &a, hipStream_t stream) {
     const Shape shape{a.batch, a.heads, a.queries, a.keys, a.radius, a.causal};
     const float scale = 1.0f / sqrtf(static_cast<float>(D));
-    const unsigned blocks = static_cast<unsigned>((a.queries + kTile - 1) / kTile) * a.batch * a.heads;
-    hipLaunchKernelGGL((attention_dq_kernel<D, MODE, VEC>), dim3(blocks), dim3(kThreads), 0, stream, tensor(a.q, a.qs),
-            tensor(a.k, a.ks), tensor(a.v, a.vs), reinterpret_cast<const uint8_t *>(a.mask), tensor(a.output, a.os), a.lse,
-            tensor(a.upstream, a.us), a.gradient_q, a.delta, shape, scale);
+    const int64_t items = static_cast<int64_t>((a.queries + kTile - 1) / kTile) * a.batch * a.heads;
+    hipLaunchKernelGGL((attention_dq_kernel<D, MODE, VEC, SPLIT>), dim3(grid_for(items, SPLIT)), dim3(kThreads), 0, stream,
+            tensor(a.q, a.qs), tensor(a.k, a.ks), tensor(a.v, a.vs), reinterpret_cast<const uint8_t *>(a.mask), tensor(a.output, a.os),
+            a.lse, tensor(a.upstream, a.us), a.gradient_q, a.delta, shape, scale);
 }
 
-template<int D, bool VEC>
+template<int D, bool VEC, int SPLIT>
 void launch_dkdv(const BackwardArgs &a, hipStream_t stream) {
     const Shape shape{a.batch, a.heads, a.queries, a.keys, a.radius, a.causal};
     const float scale = 1.0f / sqrtf(static_cast<float>(D));
-    const unsigned blocks = static_cast<unsigned>((a.keys + kTile - 1) / kTile) * a.batch * a.heads;
-    hipLaunchKernelGGL((attention_dkdv_kernel<D, VEC>), dim3(blocks), dim3(kThreads), 0, stream, tensor(a.q, a.qs), tensor(a.k, a.ks),
-            tensor(a.v, a.vs), reinterpret_cast<const uint8_t *>(a.mask), a.lse, tensor(a.upstream, a.us), a.delta, a.gradient_k,
-            a.gradient_v, shape, scale);
+    const int64_t items = static_cast<int64_t>((a.keys + kTile - 1) / kTile) * a.batch * a.heads;
+    hipLaunchKernelGGL((attention_dkdv_kernel<D, VEC, SPLIT>), dim3(grid_for(items, SPLIT)), dim3(kThreads), 0, stream, tensor(a.q, a.qs),
+            tensor(a.k, a.ks), tensor(a.v, a.vs), reinterpret_cast<const uint8_t *>(a.mask), a.lse, tensor(a.upstream, a.us), a.delta,
+            a.gradient_k, a.gradient_v, shape, scale);
 }
+
+// Waves per item: split the streamed dimension over 4 waves when the grid is too small to fill the chip with one
+// wave per item (the 24 x 1024 shapes), over 2 for mid-sized grids, not at all for large ones.
+int split_for(const int64_t items) { return items >= 4096 ? 1 : items >= 2048 ? 2 : 4; }
 
 template<int D, bool VEC>
 hipError_t run(const BackwardStage stage, const BackwardArgs &a, hipStream_t stream) {
+    const int64_t qitems = static_cast<int64_t>((a.queries + kTile - 1) / kTile) * a.batch * a.heads;
+    const int64_t kitems = static_cast<int64_t>((a.keys + kTile - 1) / kTile) * a.batch * a.heads;
     if (stage == kBackwardAll || stage == kBackwardDelta || stage == kBackwardQuery) {
-        if (stage == kBackwardAll) launch_dq<D, kDqAndDelta, VEC>(a, stream);
-        else if (stage == kBackwardDelta) launch_dq<D, kDeltaOnly, VEC>(a, stream);
-        else launch_dq<D, kDqFromDelta, VEC>(a, stream);
+        const int split = split_for(qitems);
+        if (stage == kBackwardDelta) launch_dq<D, kDeltaOnly, VEC, 1>(a, stream);
+        else if (stage == kBackwardAll) {
+            if (split == 1) launch_dq<D, kDqAndDelta, VEC, 1>(a, stream);
+            else if (split == 2) launch_dq<D, kDqAndDelta, VEC, 2>(a, stream);
+            else launch_dq<D, kDqAndDelta, VEC, 4>(a, stream);
+        } else {
+            if (split == 1) launch_dq<D, kDqFromDelta, VEC, 1>(a, stream);
+            else if (split == 2) launch_dq<D, kDqFromDelta, VEC, 2>(a, stream);
+            else launch_dq<D, kDqFromDelta, VEC, 4>(a, stream);
+        }
         const hipError_t error = hipGetLastError();
         if (error != hipSuccess || stage != kBackwardAll) return error;
     }
-    launch_dkdv<D, VEC>(a, stream);
+    const int split = split_for(kitems);
+    if (split == 1) launch_dkdv<D, VEC, 1>(a, stream);
+    else if (split == 2) launch_dkdv<D, VEC, 2>(a, stream);
+    else launch_dkdv<D, VEC, 4>(a, stream);
     return hipGetLastError();
 }
 

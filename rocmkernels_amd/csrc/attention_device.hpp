@@ -77,6 +77,7 @@ __device__ __forceinline__ const float *sequence(const Tensor &t, const int b, c
 // per-row SGPR offset replaces per-lane 64-bit address arithmetic, and the hardware range check returns 0 for
 // any access at or beyond `bytes`, so rows past the end of a sequence need no clamping and cannot fault.
 typedef __amdgpu_buffer_rsrc_t Buffer;
+constexpr uint32_t kNoRow = 0x80000000u; // voffset beyond any sequence extent (host guarantees < 2 GiB): reads 0
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kBufferWord3 = 0x00020000; // gfx9-family descriptor word 3: raw dword access
 
@@ -186,6 +187,62 @@ __device__ __forceinline__ int window_query_lo(const Shape &s, const int key) {
     return lo;
 }
 __device__ __forceinline__ int window_query_hi(const Shape &s, const int key) { return s.radius >= 0 ? key + s.radius : 0x40000000; }
+
+// ---- work mapping ------------------------------------------------------------------------------------------
+// A work item is one 32-row tile (of queries in the forward and dQ kernels, of keys in the dK/dV kernel) of one
+// (batch, head) sequence. SPLIT waves of a workgroup share an item and split its streamed tiles round-robin;
+// the workgroup's 4 waves therefore cover 4 / SPLIT items. Items are numbered rank-major (rank = position of the
+// tile in the order the caller wants them dispatched, heaviest first), sequence-minor, so with B*H a multiple of
+// 8 consecutive workgroups of one rank spread over the 8 XCDs while each XCD keeps a fixed subset of sequences.
+struct WorkItem {
+    int seq, b, head, rank, sub;
+    bool valid;
+};
+
+template<int SPLIT>
+__device__ __forceinline__ WorkItem work_item(const Shape &s, const int tiles_per_seq) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave); // wave-uniform: keeps tile bookkeeping scalar
+    const int seqs = s.batch * s.heads;
+    const int item = blockIdx.x * (kWaves / SPLIT) + wave / SPLIT;
+    WorkItem w;
+    w.sub = wave % SPLIT;
+    w.valid = item < seqs * tiles_per_seq;
+    w.rank = item / seqs;
+    w.seq = item - w.rank * seqs;
+    w.b = w.seq / s.heads;
+    w.head = w.seq - w.b * s.heads;
+    return w;
+}
+
+// Sums accumulator tiles over the SPLIT waves of an item through LDS; the wave with sub == 0 ends with the total.
+// Every wave of the workgroup must call it (it contains a workgroup barrier when SPLIT > 1).
+template<int SPLIT, int N>
+__device__ __forceinline__ void split_sum(f32x16 (&acc)[N], const int sub) {
+    if constexpr (SPLIT > 1) {
+        __shared__ float partial[kWaves][16 * N][kWave];
+        const int lane = threadIdx.x & (kWave - 1);
+        const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave); // wave-uniform: keeps tile bookkeeping scalar
+        __syncthreads(); // a previous call with the same N may still be reading `partial`
+        if (sub > 0) {
+#pragma unroll
+            for (int t = 0; t < N; ++t) {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) partial[wave][16 * t + j][lane] = acc[t][j];
+            }
+        }
+        __syncthreads();
+        if (sub == 0) {
+#pragma unroll
+            for (int w = 1; w < SPLIT; ++w) {
+#pragma unroll
+                for (int t = 0; t < N; ++t) {
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) acc[t][j] += partial[wave + w][16 * t + j][lane];
+                }
+            }
+        }
+    }
+}
 
 // True when every (query, key) pair of the 32x32 tile at (q0, key0) is inside the causal/radius window.
 __device__ __forceinline__ bool tile_in_window(const Shape &s, const int q0, const int key0) {

@@ -30,7 +30,7 @@ __global__ __launch_bounds__(kThreads) void attention_forward_kernel(const Tenso
     constexpr int NREG = STATS ? 0 : 16 * DT;
 
     const int lane = threadIdx.x & (kWave - 1);
-    const int wave = threadIdx.x / kWave;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave); // wave-uniform: keeps tile bookkeeping scalar
     const int col = lane & 31;
     const int h = lane >> 5;
 
@@ -66,49 +66,56 @@ __global__ __launch_bounds__(kThreads) void attention_forward_kernel(const Tenso
     float qr[HALF];
     buffer_load_span<VEC>(qr, qbuf, static_cast<uint32_t>(query) * (4u * q.st) + 4u * h * HALF); // rows >= queries read 0
 
-    // Online-softmax state of this lane's query over the tiles this wave visits. m_run is the raw maximum of
-    // q·k; mc_run = m_run·c2 rounded once, the exponent offset every p = exp2(s·c2 - mc) of the state uses, so
-    // that alpha = exp2(mc_old - mc_new) is exactly 1 when the maximum does not move.
+    // Online-softmax state of this lane's query over the tiles this wave visits. m_run is the raw maximum of q·k.
+    // The exponentials are taken against a reference offset mc (in log2 units, c2-scaled): p = exp2(s·c2 - mc).
+    // mc moves only when the running maximum exceeds it by more than kLazy (so p <= 2^kLazy, far from overflow);
+    // o and l are then rescaled by exp2(mc_old - mc_new). The lse sum is brought to the true maximum once at
+    // the end. Skipping most rescales removes 16·D/32 VALU multiplies per tile, which matters because FP32 MFMA
+    // and VALU share the SIMD on gfx950: every VALU cycle adds to the MFMA time.
+    constexpr float kLazy = 8.0f;
     float m_run = -INFINITY;
-    float mc_run = -INFINITY;
+    float mc = -INFINITY; // offset of the state; -inf until the row has a visible key
+    float mcx = 0.0f;     // finite stand-in used in the exponent (masked scores are -inf there, giving 0)
     float l_run = 0.0f;
     f32x16 o[DT];
 #pragma unroll
     for (int t = 0; t < DT; ++t) o[t] = f32x16{};
 
-    // K rows (Sᵀ A operand, row layout) and the mask byte of a tile are loaded one tile ahead; V (PV A operand,
-    // column layout) is loaded at the start of its own tile and lands while Sᵀ and the softmax run.
-    auto load_k = [&](float (&kr)[HALF], int &mb, const int key0) __attribute__((always_inline)) {
-        const uint32_t key = static_cast<uint32_t>(key0 + col);
-        mb = buffer_load_byte(mbuf, key); // keys >= s.keys read 0: masked
-        buffer_load_span<VEC>(kr, kbuf, key * kstep + 4u * h * HALF);
+    // K rows (Sᵀ A operand, row layout), V columns (PV A operand) and the mask byte of the tile after next are
+    // loaded while the current tile computes. The loads are unconditional: past the last tile they read rows
+    // that are never used (or, beyond the sequence, zeros), which keeps the two register sets free of copies.
+    struct Tile {
+        float k[HALF];
+        float v[STATS ? 1 : DT][16];
+        int mask;
     };
-
-    // prefetch() issues the next tile's K/mask loads. It runs after this tile's V loads and Sᵀ MFMAs are issued:
-    // vector-memory counters complete in order, so loads issued earlier than this tile's V would make the PV
-    // MFMAs wait for them.
-    auto step = [&](const float (&kr)[HALF], const int mb, const int key0, auto prefetch) __attribute__((always_inline)) {
-        const uint32_t bits = static_cast<uint32_t>(__ballot(mb != 0));
-        if (bits == 0) { // every key of the tile is masked: contributes nothing
-            prefetch();
-            return;
-        }
-
-        float vc[STATS ? 1 : DT][16];
+    auto load_tile = [&](Tile &t, const int key0) __attribute__((always_inline)) {
+        const uint32_t key = static_cast<uint32_t>(key0 + col);
+        t.mask = buffer_load_byte(mbuf, key); // keys >= s.keys read 0: masked
+        buffer_load_span<VEC>(t.k, kbuf, key * kstep + 4u * h * HALF);
         if constexpr (!STATS) {
             const uint32_t vlane = static_cast<uint32_t>(key0 + 4 * h) * vstep + 4u * col;
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
 #pragma unroll
-                for (int t = 0; t < DT; ++t) vc[t][j] = buffer_load(vbuf, vlane + 128u * t, static_cast<uint32_t>(8 * (j >> 2) + (j & 3)) * vstep);
+                for (int t2 = 0; t2 < DT; ++t2)
+                    t.v[t2][j] = buffer_load(vbuf, vlane + 128u * t2, static_cast<uint32_t>(8 * (j >> 2) + (j & 3)) * vstep);
             }
         }
+    };
 
+    auto step = [&](Tile &t, const int key0, Tile &next, const int next_key0) __attribute__((always_inline)) {
+        // key0 >= last marks the padding step of a wave with an odd number of tiles.
+        const uint32_t bits = key0 < last ? static_cast<uint32_t>(__ballot(t.mask != 0)) : 0u;
+        if (bits == 0) { // every key of the tile is masked: contributes nothing
+            load_tile(next, next_key0);
+            return;
+        }
         f32x16 sc{};
 #pragma unroll
-        for (int c = 0; c < HALF; ++c) sc = mfma(kr[c], qr[c], sc);
+        for (int c = 0; c < HALF; ++c) sc = mfma(t.k[c], qr[c], sc);
         __builtin_amdgcn_sched_barrier(0);
-        prefetch();
+        load_tile(next, next_key0);
         __builtin_amdgcn_sched_barrier(0);
 
         if (bits != 0xffffffffu || !tile_in_window(s, q0, key0)) {
@@ -123,7 +130,7 @@ __global__ __launch_bounds__(kThreads) void attention_forward_kernel(const Tenso
 #pragma unroll
                     for (int j = 0; j < 16; ++j) {
 #pragma unroll
-                        for (int t = 0; t < DT; ++t) vc[t][j] = (kept >> (8 * (j >> 2) + (j & 3))) & 1u ? vc[t][j] : 0.0f;
+                        for (int t2 = 0; t2 < DT; ++t2) t.v[t2][j] = (kept >> (8 * (j >> 2) + (j & 3))) & 1u ? t.v[t2][j] : 0.0f;
                     }
                 }
             }
@@ -133,55 +140,62 @@ __global__ __launch_bounds__(kThreads) void attention_forward_kernel(const Tenso
 #pragma unroll
         for (int j = 1; j < 16; ++j) mx = fmaxf(mx, sc[j]);
         mx = halves_max(mx);
-        const float m_new = fmaxf(m_run, mx);
-        const float mc = m_new == -INFINITY ? 0.0f : m_new * c2;
-        const float alpha = exp2_fast(mc_run - mc);
-        float psum = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            sc[j] = exp2_fast(fmaf(sc[j], c2, -mc));
-            psum += sc[j];
-        }
-        l_run = fmaf(l_run, alpha, psum);
-        m_run = m_new;
-        mc_run = m_new == -INFINITY ? -INFINITY : mc;
+        m_run = fmaxf(m_run, mx);
 
-        if constexpr (!STATS) {
-            if (__ballot(alpha != 1.0f) != 0) {
-#pragma unroll
-                for (int t = 0; t < DT; ++t) o[t] *= alpha;
-            }
+        // exp, row sum and PV; instantiated on both sides of the re-base branch so that each side ends in the
+        // MFMA chain that writes o (a join after a conditional o *= alpha would cost a copy of o on every tile).
+        auto finish = [&]() __attribute__((always_inline)) {
+            float psum = 0.0f;
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
-#pragma unroll
-                for (int t = 0; t < DT; ++t) o[t] = mfma(vc[t][j], sc[j], o[t]);
+                sc[j] = exp2_fast(fmaf(sc[j], c2, -mcx));
+                psum += sc[j];
             }
+            l_run += psum;
+            if constexpr (!STATS) {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+#pragma unroll
+                    for (int t2 = 0; t2 < DT; ++t2) o[t2] = mfma(t.v[t2][j], sc[j], o[t2]);
+                }
+            }
+        };
+        if (__ballot(m_run * c2 > mc + kLazy) != 0) {
+            // Re-base every lane on its current maximum. A row without a visible key yet keeps offset -inf (its
+            // l and o are 0); the first finite offset multiplies them by exp2(-inf) = 0.
+            const float mc_new = m_run == -INFINITY ? -INFINITY : m_run * c2;
+            const float alpha = mc_new == -INFINITY ? 1.0f : exp2_fast(mc - mc_new);
+            l_run *= alpha;
+            if constexpr (!STATS) {
+#pragma unroll
+                for (int t2 = 0; t2 < DT; ++t2) o[t2] *= alpha;
+            }
+            mc = mc_new;
+            mcx = mc_new == -INFINITY ? 0.0f : mc_new;
+            finish();
+        } else {
+            finish();
         }
     };
 
-    float ka[HALF], kb[HALF];
-    int ma = 0, mb = 0;
-    int tile = wave;
-    if (tile < ntiles) load_k(ka, ma, first + tile * kTile);
-    while (tile < ntiles) {
-        int next = tile + kWaves;
-        step(ka, ma, first + tile * kTile, [&] {
-            if (next < ntiles) load_k(kb, mb, first + next * kTile);
-        });
-        tile = next;
-        if (tile >= ntiles) break;
-        next = tile + kWaves;
-        step(kb, mb, first + tile * kTile, [&] {
-            if (next < ntiles) load_k(ka, ma, first + next * kTile);
-        });
-        tile = next;
+    // The wave visits tiles wave, wave + kWaves, ...; their count is rounded up to even so the loop body is two
+    // straight-line steps (the padding step sees no key).
+    const int mine = ntiles > wave ? (ntiles - wave + kWaves - 1) / kWaves : 0;
+    Tile ta, tb;
+    if (mine > 0) load_tile(ta, first + wave * kTile);
+    for (int i = 0; i < mine; i += 2) {
+        const int key0 = first + (wave + i * kWaves) * kTile;
+        step(ta, key0, tb, key0 + kWaves * kTile);
+        step(tb, key0 + kWaves * kTile, ta, key0 + 2 * kWaves * kTile);
     }
+    const float mc_run = mc; // offset the wave's (l_run, o) are expressed against
 
     // Merge the per-wave states of the workgroup: waves 1..3 publish (m, l, Oᵀ) in LDS, wave 0 combines.
-    __shared__ float partial[kWaves - 1][NREG + 2][kWave];
+    __shared__ float partial[kWaves - 1][NREG + 3][kWave];
     if (wave > 0) {
         partial[wave - 1][0][lane] = m_run;
         partial[wave - 1][1][lane] = l_run;
+        partial[wave - 1][2 + NREG][lane] = mc_run;
         if constexpr (!STATS) {
 #pragma unroll
             for (int t = 0; t < DT; ++t) {
@@ -193,11 +207,17 @@ __global__ __launch_bounds__(kThreads) void attention_forward_kernel(const Tenso
     __syncthreads();
     if (wave != 0) return;
 
+    // Every state (m_w, mc_w, l_w, o_w) satisfies l_w = Σ exp2(s·c2 - mc_w); combine them against the largest
+    // offset, then express the sum against the true maximum for lse.
     float m_all = m_run;
+    float mc_all = mc_run;
 #pragma unroll
-    for (int w = 0; w < kWaves - 1; ++w) m_all = fmaxf(m_all, partial[w][0][lane]);
-    const float mc_all = m_all == -INFINITY ? 0.0f : m_all * c2;
-    const float a0 = exp2_fast(mc_run - mc_all);
+    for (int w = 0; w < kWaves - 1; ++w) {
+        m_all = fmaxf(m_all, partial[w][0][lane]);
+        mc_all = fmaxf(mc_all, partial[w][2 + NREG][lane]);
+    }
+    const float base = mc_all == -INFINITY ? 0.0f : mc_all;
+    const float a0 = exp2_fast(mc_run - base);
     float l_all = l_run * a0;
     if constexpr (!STATS) {
 #pragma unroll
@@ -205,8 +225,7 @@ __global__ __launch_bounds__(kThreads) void attention_forward_kernel(const Tenso
     }
 #pragma unroll
     for (int w = 0; w < kWaves - 1; ++w) {
-        const float mw = partial[w][0][lane];
-        const float aw = exp2_fast((mw == -INFINITY ? -INFINITY : mw * c2) - mc_all);
+        const float aw = exp2_fast(partial[w][2 + NREG][lane] - base);
         l_all = fmaf(partial[w][1][lane], aw, l_all);
         if constexpr (!STATS) {
 #pragma unroll
@@ -217,6 +236,8 @@ __global__ __launch_bounds__(kThreads) void attention_forward_kernel(const Tenso
         }
     }
     l_all = halves_sum(l_all); // each half-wave summed the exponentials of its own 16 keys per tile
+    // O is o / l in any offset; lse's sum is Σ exp(s - max) = l · exp2(offset - max·c2).
+    const float sum_at_max = m_all == -INFINITY ? l_all : l_all * exp2_fast(base - m_all * c2);
 
     if (query >= s.queries) return;
     const bool nan_row = isnan(l_all);
@@ -237,7 +258,7 @@ __global__ __launch_bounds__(kThreads) void attention_forward_kernel(const Tenso
     if (h == 0) {
         const int64_t row = static_cast<int64_t>(seq) * s.queries + query;
         lse[2 * row] = has_keys ? m_all * scale : (nan_row ? NAN : -INFINITY);
-        lse[2 * row + 1] = has_keys ? l_all : (nan_row ? NAN : 0.0f);
+        lse[2 * row + 1] = has_keys ? sum_at_max : (nan_row ? NAN : 0.0f);
     }
 }
 

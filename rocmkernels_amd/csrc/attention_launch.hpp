@@ -25,11 +25,12 @@ struct BackwardArgs {
     rocmkernels_strides qs, ks, vs, os, us;
 };
 
-// Buffer resources address one (batch, head) sequence with 32-bit byte offsets: every sequence of every
-// tensor must span less than 4 GiB ((rows - 1) * token stride + D floats).
+// Buffer resources address one (batch, head) sequence with 32-bit byte offsets. Kernels read up to one 32-row
+// tile past the end (those reads return 0) and use offset 2^31 as "no row", so every sequence of every tensor,
+// padded by one tile, must span less than 2 GiB.
 inline bool sequence_fits(const int rows, const rocmkernels_strides &s, const int width) {
-    const long long extent = (static_cast<long long>(rows) - 1) * s.token + width;
-    return s.token >= 0 && extent * 4 < (1ll << 32);
+    const long long extent = (static_cast<long long>(rows) + 32) * s.token + width;
+    return s.token >= 0 && extent * 4 < (1ll << 31);
 }
 
 // Forward pass for head width D (32 or 64). statistics_only writes lse and skips V and the output.
