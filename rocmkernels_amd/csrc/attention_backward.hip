@@ -68,9 +68,9 @@ __global__ __launch_bounds__(kThreads) void attention_dq_kernel(const Tensor q, 
     buffer_load_span<VEC>(qr, qbuf, qvalid ? static_cast<uint32_t>(query) * (4u * q.st) + 4u * h * HALF : kNoRow);
     const float m = qvalid ? lse[2 * row] : -INFINITY;
     const float l = qvalid ? lse[2 * row + 1] : 0.0f;
-    const bool row_ok = m != -INFINITY;
-    const float mc = row_ok ? m * kLog2e : INFINITY; // exp2(x - inf) = 0 for a row without visible keys
-    const float il = row_ok ? 1.0f / l : 0.0f;
+    // P = exp(s - m) / l = exp2(s·c2 - (m·log2e + log2 l)): the normaliser folds into the exponent offset.
+    // A row without visible keys gets offset +inf, so exp2(x - inf) = 0.
+    const float mc = m != -INFINITY ? fmaf(m, kLog2e, __log2f(l)) : INFINITY;
 
     int first = 0, last = s.keys;
     if (s.radius >= 0) {
@@ -100,11 +100,13 @@ __global__ __launch_bounds__(kThreads) void attention_dq_kernel(const Tensor q, 
         buffer_load_span<VEC>(vr, vbuf, key * vstep + 4u * h * HALF);
     };
 
-    auto step = [&](const float (&kr)[HALF], const float (&vr)[HALF], const int mb, const int key0, auto prefetch)
-            __attribute__((always_inline)) {
-        const uint32_t bits = static_cast<uint32_t>(__ballot(mb != 0));
+    // One key tile; the next tile's rows are loaded into the other register set after the MFMAs are issued.
+    // key0 >= last marks the padding step of a wave with an odd number of tiles.
+    auto step = [&](const float (&kr)[HALF], const float (&vr)[HALF], const int mb, const int key0, float (&kn)[HALF],
+                        float (&vn)[HALF], int &mn, const int next_key0) __attribute__((always_inline)) {
+        const uint32_t bits = key0 < last ? static_cast<uint32_t>(__ballot(mb != 0)) : 0u;
         if (bits == 0) {
-            prefetch();
+            load_rows(kn, vn, mn, next_key0);
             return;
         }
         // K in column layout (dQᵀ A operand): row key0 + tile_row(j, h), feature 32t + col.
@@ -123,12 +125,12 @@ __global__ __launch_bounds__(kThreads) void attention_dq_kernel(const Tensor q, 
             dp = mfma(vr[c], dor[c], dp);
         }
         __builtin_amdgcn_sched_barrier(0);
-        prefetch();
+        load_rows(kn, vn, mn, next_key0);
         __builtin_amdgcn_sched_barrier(0);
 
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-            const float p = exp2_fast(fmaf(sc[j], c2, -mc)) * il;
+            const float p = exp2_fast(fmaf(sc[j], c2, -mc));
             sc[j] = p * (dp[j] - dlt);
         }
         if (bits != 0xffffffffu || !tile_in_window(s, q0, key0)) {
@@ -151,22 +153,15 @@ __global__ __launch_bounds__(kThreads) void attention_dq_kernel(const Tensor q, 
         }
     };
 
+    // Tiles sub, sub + SPLIT, ...; the count is rounded up to even so the loop body is two straight-line steps.
+    const int mine = ntiles > w.sub ? (ntiles - w.sub + SPLIT - 1) / SPLIT : 0;
     float ka[HALF], va[HALF], kb[HALF], vb[HALF];
     int ma = 0, mb = 0;
-    int tile = w.sub;
-    if (tile < ntiles) load_rows(ka, va, ma, first + tile * kTile);
-    while (tile < ntiles) {
-        int next = tile + SPLIT;
-        step(ka, va, ma, first + tile * kTile, [&] {
-            if (next < ntiles) load_rows(kb, vb, mb, first + next * kTile);
-        });
-        tile = next;
-        if (tile >= ntiles) break;
-        next = tile + SPLIT;
-        step(kb, vb, mb, first + tile * kTile, [&] {
-            if (next < ntiles) load_rows(ka, va, ma, first + next * kTile);
-        });
-        tile = next;
+    if (mine > 0) load_rows(ka, va, ma, first + w.sub * kTile);
+    for (int i = 0; i < mine; i += 2) {
+        const int key0 = first + (w.sub + i * SPLIT) * kTile;
+        step(ka, va, ma, key0, kb, vb, mb, key0 + SPLIT * kTile);
+        step(kb, vb, mb, key0 + SPLIT * kTile, ka, va, ma, key0 + 2 * SPLIT * kTile);
     }
 
     split_sum<SPLIT>(acc, w.sub);
@@ -212,9 +207,10 @@ __global__ __launch_bounds__(kThreads) void attention_dkdv_kernel(const Tensor q
     }
     first = max(first, 0);
     const int ntiles = (bits != 0 && last > first) ? (last - first + kTile - 1) / kTile : 0;
-    // Queries that see this lane's key: [qlo, qhi] (also capped at the last query).
+    // Queries that see this lane's key: [qlo, qhi] (also capped at the last query of the range).
     const int qlo = window_query_lo(s, key);
-    const int qhi = min(window_query_hi(s, key), s.queries - 1);
+    const int qhi = min(window_query_hi(s, key), last - 1);
+
 
     const Buffer qbuf = make_buffer(sequence(q, w.b, w.head), sequence_bytes(s.queries, q.st, D));
     const Buffer ubuf = make_buffer(sequence(du, w.b, w.head), sequence_bytes(s.queries, du.st, D));
@@ -223,7 +219,7 @@ __global__ __launch_bounds__(kThreads) void attention_dkdv_kernel(const Tensor q
     const uint32_t qstep = 4u * q.st;
     const uint32_t ustep = 4u * du.st;
 
-    __shared__ __align__(16) float stats[kWaves][3][kTile];
+    __shared__ __align__(16) float stats[kWaves][2][kTile];
 
     f32x16 acc_k[DT], acc_v[DT];
 #pragma unroll
@@ -246,15 +242,17 @@ __global__ __launch_bounds__(kThreads) void attention_dkdv_kernel(const Tensor q
         r.d = buffer_load(dbuf, qq * 4u, 0);
     };
 
-    auto step = [&](const Rows &r, const int q0, auto prefetch) __attribute__((always_inline)) {
+    // One query tile; the next tile's rows are loaded into the other set after the MFMAs are issued. q0 >= last
+    // marks the padding step of a wave with an odd number of tiles (the kernel has no masked-query skip: a
+    // padding step computes zeros).
+    auto step = [&](const Rows &r, const int q0, Rows &next, const int next_q0) __attribute__((always_inline)) {
         // Per-query constants for the 32 queries of the tile, staged in this wave's LDS slice and read back in
         // accumulator order (lane needs queries q0 + tile_row(j, h)). Queries past the end get exp2(-inf) = 0.
         wave_lds_sync();
         if (h == 0) {
-            const bool ok = q0 + col < s.queries && r.m != -INFINITY;
-            stats[wave][0][col] = ok ? r.m * kLog2e : INFINITY;
-            stats[wave][1][col] = ok ? 1.0f / r.l : 0.0f;
-            stats[wave][2][col] = r.d;
+            const bool ok = q0 + col < last && r.m != -INFINITY;
+            stats[wave][0][col] = ok ? fmaf(r.m, kLog2e, __log2f(r.l)) : INFINITY; // exp2(s·c2 - this) = P
+            stats[wave][1][col] = r.d;
         }
         wave_lds_sync();
 
@@ -279,23 +277,22 @@ __global__ __launch_bounds__(kThreads) void attention_dkdv_kernel(const Tensor q
             dp = mfma(r.ur[c], vr[c], dp);
         }
         __builtin_amdgcn_sched_barrier(0);
-        prefetch();
+        load_rows(next, next_q0);
         __builtin_amdgcn_sched_barrier(0);
 
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const f32x4 mcs = *reinterpret_cast<const f32x4 *>(&stats[wave][0][8 * u + 4 * h]);
-            const f32x4 ils = *reinterpret_cast<const f32x4 *>(&stats[wave][1][8 * u + 4 * h]);
-            const f32x4 dls = *reinterpret_cast<const f32x4 *>(&stats[wave][2][8 * u + 4 * h]);
+            const f32x4 dls = *reinterpret_cast<const f32x4 *>(&stats[wave][1][8 * u + 4 * h]);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int j = 4 * u + i;
-                const float p = exp2_fast(fmaf(sc[j], c2, -mcs[i])) * ils[i];
+                const float p = exp2_fast(fmaf(sc[j], c2, -mcs[i]));
                 sc[j] = p;
                 dp[j] = p * (dp[j] - dls[i]);
             }
         }
-        if (bits != 0xffffffffu || q0 + kTile > s.queries || !tile_in_window(s, q0, key0)) {
+        if (bits != 0xffffffffu || q0 + kTile > last || !tile_in_window(s, q0, key0)) {
             const uint32_t keep = visible ? bit_range(qlo - q0, qhi - q0) >> (4 * h) : 0u;
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
@@ -314,21 +311,14 @@ __global__ __launch_bounds__(kThreads) void attention_dkdv_kernel(const Tensor q
         }
     };
 
+    // Tiles sub, sub + SPLIT, ...; the count is rounded up to even so the loop body is two straight-line steps.
+    const int mine = ntiles > w.sub ? (ntiles - w.sub + SPLIT - 1) / SPLIT : 0;
     Rows ra, rb;
-    int tile = w.sub;
-    if (tile < ntiles) load_rows(ra, first + tile * kTile);
-    while (tile < ntiles) {
-        int next = tile + SPLIT;
-        step(ra, first + tile * kTile, [&] {
-            if (next < ntiles) load_rows(rb, first + next * kTile);
-        });
-        tile = next;
-        if (tile >= ntiles) break;
-        next = tile + SPLIT;
-        step(rb, first + tile * kTile, [&] {
-            if (next < ntiles) load_rows(ra, first + next * kTile);
-        });
-        tile = next;
+    if (mine > 0) load_rows(ra, first + w.sub * kTile);
+    for (int i = 0; i < mine; i += 2) {
+        const int q0 = first + (w.sub + i * SPLIT) * kTile;
+        step(ra, q0, rb, q0 + SPLIT * kTile);
+        step(rb, q0 + SPLIT * kTile, ra, q0 + 2 * SPLIT * kTile);
     }
 
     split_sum<SPLIT>(acc_k, w.sub);
@@ -349,14 +339,13 @@ bool strides4(const rocmkernels_strides &s) { return ((s.batch | s.head | s.toke
 
 Tensor tensor(const float *p, const rocmkernels_strides &s) { return Tensor{p, s.batch, s.head, s.token}; }
 
-unsigned grid_for(const int64_t items, const int split) { return static_cast<unsigned>((items + kWaves / split - 1) / (kWaves / split)); }
 
 template<int D, int MODE, bool VEC, int SPLIT>
 void launch_dq(const BackwardArgs &a, hipStream_t stream) {
     const Shape shape{a.batch, a.heads, a.queries, a.keys, a.radius, a.causal};
     const float scale = 1.0f / sqrtf(static_cast<float>(D));
     const int64_t items = static_cast<int64_t>((a.queries + kTile - 1) / kTile) * a.batch * a.heads;
-    hipLaunchKernelGGL((attention_dq_kernel<D, MODE, VEC, SPLIT>), dim3(grid_for(items, SPLIT)), dim3(kThreads), 0, stream,
+    hipLaunchKernelGGL((attention_dq_kernel<D, MODE, VEC, SPLIT>), dim3(workgroups_for(items, SPLIT)), dim3(kThreads), 0, stream,
             tensor(a.q, a.qs), tensor(a.k, a.ks), tensor(a.v, a.vs), reinterpret_cast<const uint8_t *>(a.mask), tensor(a.output, a.os),
             a.lse, tensor(a.upstream, a.us), a.gradient_q, a.delta, shape, scale);
 }
@@ -366,14 +355,11 @@ void launch_dkdv(const BackwardArgs &a, hipStream_t stream) {
     const Shape shape{a.batch, a.heads, a.queries, a.keys, a.radius, a.causal};
     const float scale = 1.0f / sqrtf(static_cast<float>(D));
     const int64_t items = static_cast<int64_t>((a.keys + kTile - 1) / kTile) * a.batch * a.heads;
-    hipLaunchKernelGGL((attention_dkdv_kernel<D, VEC, SPLIT>), dim3(grid_for(items, SPLIT)), dim3(kThreads), 0, stream, tensor(a.q, a.qs),
+    hipLaunchKernelGGL((attention_dkdv_kernel<D, VEC, SPLIT>), dim3(workgroups_for(items, SPLIT)), dim3(kThreads), 0, stream, tensor(a.q, a.qs),
             tensor(a.k, a.ks), tensor(a.v, a.vs), reinterpret_cast<const uint8_t *>(a.mask), a.lse, tensor(a.upstream, a.us), a.delta,
             a.gradient_k, a.gradient_v, shape, scale);
 }
 
-// Waves per item: split the streamed dimension over 4 waves when the grid is too small to fill the chip with one
-// wave per item (the 24 x 1024 shapes), over 2 for mid-sized grids, not at all for large ones.
-int split_for(const int64_t items) { return items >= 4096 ? 1 : items >= 2048 ? 2 : 4; }
 
 template<int D, bool VEC>
 hipError_t run(const BackwardStage stage, const BackwardArgs &a, hipStream_t stream) {

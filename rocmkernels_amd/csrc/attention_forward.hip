@@ -21,7 +21,7 @@
 
 namespace rk {
 
-template<int D, bool STATS, bool VEC>
+template<int D, bool STATS, bool VEC, int SPLIT>
 __global__ __launch_bounds__(kThreads) void attention_forward_kernel(const Tensor q, const Tensor k, const Tensor v,
         const uint8_t *__restrict__ mask, float *__restrict__ out, const int osb, const int osh, const int ost,
         float *__restrict__ lse, const Shape s, const float scale) {
@@ -34,13 +34,10 @@ __global__ __launch_bounds__(kThreads) void attention_forward_kernel(const Tenso
     const int col = lane & 31;
     const int h = lane >> 5;
 
-    const int seqs = s.batch * s.heads;
     const int qtiles = (s.queries + kTile - 1) / kTile;
-    const int rank = blockIdx.x / seqs;
-    const int seq = blockIdx.x - rank * seqs;
-    const int qt = s.causal ? qtiles - 1 - rank : rank;
-    const int b = seq / s.heads;
-    const int head = seq - b * s.heads;
+    const WorkItem w = work_item<SPLIT>(s, qtiles);
+    const int seq = w.seq, b = w.b, head = w.head, sub = w.sub;
+    const int qt = s.causal ? qtiles - 1 - w.rank : w.rank;
     const int q0 = qt * kTile;
     const int query = q0 + col;
     const float c2 = scale * kLog2e;
@@ -51,7 +48,7 @@ __global__ __launch_bounds__(kThreads) void attention_forward_kernel(const Tenso
         last = min(last, q0 + kTile + s.radius);
     }
     if (s.causal) last = min(last, q0 + kTile);
-    const int ntiles = last > first ? (last - first + kTile - 1) / kTile : 0;
+    const int ntiles = (w.valid && last > first) ? (last - first + kTile - 1) / kTile : 0;
     // This lane's query sees keys [wlo, whi] through the causal/radius window.
     const int wlo = window_lo(s, query);
     const int whi = window_hi(s, query);
@@ -178,68 +175,72 @@ __global__ __launch_bounds__(kThreads) void attention_forward_kernel(const Tenso
         }
     };
 
-    // The wave visits tiles wave, wave + kWaves, ...; their count is rounded up to even so the loop body is two
+    // The wave visits tiles sub, sub + SPLIT, ...; their count is rounded up to even so the loop body is two
     // straight-line steps (the padding step sees no key).
-    const int mine = ntiles > wave ? (ntiles - wave + kWaves - 1) / kWaves : 0;
+    const int mine = ntiles > sub ? (ntiles - sub + SPLIT - 1) / SPLIT : 0;
     Tile ta, tb;
-    if (mine > 0) load_tile(ta, first + wave * kTile);
+    if (mine > 0) load_tile(ta, first + sub * kTile);
     for (int i = 0; i < mine; i += 2) {
-        const int key0 = first + (wave + i * kWaves) * kTile;
-        step(ta, key0, tb, key0 + kWaves * kTile);
-        step(tb, key0 + kWaves * kTile, ta, key0 + 2 * kWaves * kTile);
+        const int key0 = first + (sub + i * SPLIT) * kTile;
+        step(ta, key0, tb, key0 + SPLIT * kTile);
+        step(tb, key0 + SPLIT * kTile, ta, key0 + 2 * SPLIT * kTile);
     }
     const float mc_run = mc; // offset the wave's (l_run, o) are expressed against
 
-    // Merge the per-wave states of the workgroup: waves 1..3 publish (m, l, Oᵀ) in LDS, wave 0 combines.
-    __shared__ float partial[kWaves - 1][NREG + 3][kWave];
-    if (wave > 0) {
-        partial[wave - 1][0][lane] = m_run;
-        partial[wave - 1][1][lane] = l_run;
-        partial[wave - 1][2 + NREG][lane] = mc_run;
-        if constexpr (!STATS) {
-#pragma unroll
-            for (int t = 0; t < DT; ++t) {
-#pragma unroll
-                for (int j = 0; j < 16; ++j) partial[wave - 1][2 + 16 * t + j][lane] = o[t][j];
-            }
-        }
-    }
-    __syncthreads();
-    if (wave != 0) return;
-
-    // Every state (m_w, mc_w, l_w, o_w) satisfies l_w = Σ exp2(s·c2 - mc_w); combine them against the largest
-    // offset, then express the sum against the true maximum for lse.
+    // Merge the states of the SPLIT waves of the item: waves with sub > 0 publish (m, l, mc, Oᵀ) in LDS, the
+    // wave with sub == 0 combines. Every state satisfies l_w = Σ exp2(s·c2 - mc_w); they are combined against the
+    // largest offset, and lse's sum is then expressed against the true maximum.
     float m_all = m_run;
     float mc_all = mc_run;
+    float base = 0.0f, l_all = l_run;
+    if constexpr (SPLIT > 1) {
+        __shared__ float partial[kWaves][NREG + 3][kWave];
+        if (sub > 0) {
+            partial[wave][0][lane] = m_run;
+            partial[wave][1][lane] = l_run;
+            partial[wave][2 + NREG][lane] = mc_run;
+            if constexpr (!STATS) {
 #pragma unroll
-    for (int w = 0; w < kWaves - 1; ++w) {
-        m_all = fmaxf(m_all, partial[w][0][lane]);
-        mc_all = fmaxf(mc_all, partial[w][2 + NREG][lane]);
-    }
-    const float base = mc_all == -INFINITY ? 0.0f : mc_all;
-    const float a0 = exp2_fast(mc_run - base);
-    float l_all = l_run * a0;
-    if constexpr (!STATS) {
+                for (int t = 0; t < DT; ++t) {
 #pragma unroll
-        for (int t = 0; t < DT; ++t) o[t] *= a0;
-    }
-#pragma unroll
-    for (int w = 0; w < kWaves - 1; ++w) {
-        const float aw = exp2_fast(partial[w][2 + NREG][lane] - base);
-        l_all = fmaf(partial[w][1][lane], aw, l_all);
-        if constexpr (!STATS) {
-#pragma unroll
-            for (int t = 0; t < DT; ++t) {
-#pragma unroll
-                for (int j = 0; j < 16; ++j) o[t][j] = fmaf(partial[w][2 + 16 * t + j][lane], aw, o[t][j]);
+                    for (int j = 0; j < 16; ++j) partial[wave][2 + 16 * t + j][lane] = o[t][j];
+                }
             }
         }
+        __syncthreads();
+        if (sub != 0) return;
+#pragma unroll
+        for (int x = 1; x < SPLIT; ++x) {
+            m_all = fmaxf(m_all, partial[wave + x][0][lane]);
+            mc_all = fmaxf(mc_all, partial[wave + x][2 + NREG][lane]);
+        }
+        base = mc_all == -INFINITY ? 0.0f : mc_all;
+        const float a0 = exp2_fast(mc_run - base);
+        l_all = l_run * a0;
+        if constexpr (!STATS) {
+#pragma unroll
+            for (int t = 0; t < DT; ++t) o[t] *= a0;
+        }
+#pragma unroll
+        for (int x = 1; x < SPLIT; ++x) {
+            const float aw = exp2_fast(partial[wave + x][2 + NREG][lane] - base);
+            l_all = fmaf(partial[wave + x][1][lane], aw, l_all);
+            if constexpr (!STATS) {
+#pragma unroll
+                for (int t = 0; t < DT; ++t) {
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) o[t][j] = fmaf(partial[wave + x][2 + 16 * t + j][lane], aw, o[t][j]);
+                }
+            }
+        }
+    } else {
+        base = mc_run == -INFINITY ? 0.0f : mc_run;
     }
     l_all = halves_sum(l_all); // each half-wave summed the exponentials of its own 16 keys per tile
     // O is o / l in any offset; lse's sum is Σ exp(s - max) = l · exp2(offset - max·c2).
     const float sum_at_max = m_all == -INFINITY ? l_all : l_all * exp2_fast(base - m_all * c2);
 
-    if (query >= s.queries) return;
+    if (!w.valid || query >= s.queries) return;
     const bool nan_row = isnan(l_all);
     const bool has_keys = l_all > 0.0f;
     if constexpr (!STATS) {
@@ -267,25 +268,35 @@ namespace {
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 bool strides4(const rocmkernels_strides &s) { return ((s.batch | s.head | s.token) & 3) == 0; }
 
-template<int D, bool STATS, bool VEC>
-void launch(const ForwardArgs &a, const dim3 grid, hipStream_t stream) {
+template<int D, bool STATS, bool VEC, int SPLIT>
+void launch(const ForwardArgs &a, const int64_t items, hipStream_t stream) {
     const Shape shape{a.batch, a.heads, a.queries, a.keys, a.radius, a.causal};
     const float scale = 1.0f / sqrtf(static_cast<float>(D));
-    hipLaunchKernelGGL((attention_forward_kernel<D, STATS, VEC>), grid, dim3(kThreads), 0, stream, Tensor{a.q, a.qs.batch, a.qs.head, a.qs.token},
-            Tensor{a.k, a.ks.batch, a.ks.head, a.ks.token}, Tensor{a.v, a.vs.batch, a.vs.head, a.vs.token},
-            reinterpret_cast<const uint8_t *>(a.mask), a.output, a.os.batch, a.os.head, a.os.token, a.lse, shape, scale);
+    hipLaunchKernelGGL((attention_forward_kernel<D, STATS, VEC, SPLIT>), dim3(workgroups_for(items, SPLIT)), dim3(kThreads),
+            0, stream, Tensor{a.q, a.qs.batch, a.qs.head, a.qs.token}, Tensor{a.k, a.ks.batch, a.ks.head, a.ks.token},
+            Tensor{a.v, a.vs.batch, a.vs.head, a.vs.token}, reinterpret_cast<const uint8_t *>(a.mask), a.output, a.os.batch,
+            a.os.head, a.os.token, a.lse, shape, scale);
+}
+
+template<int D, bool STATS, bool VEC>
+void launch_split(const ForwardArgs &a, const int64_t items, hipStream_t stream) {
+    switch (split_for(items)) {
+        case 1: launch<D, STATS, VEC, 1>(a, items, stream); break;
+        case 2: launch<D, STATS, VEC, 2>(a, items, stream); break;
+        default: launch<D, STATS, VEC, 4>(a, items, stream); break;
+    }
 }
 
 template<int D>
-void dispatch(const bool statistics_only, const ForwardArgs &a, const dim3 grid, hipStream_t stream) {
+void dispatch(const bool statistics_only, const ForwardArgs &a, const int64_t items, hipStream_t stream) {
     bool vec = aligned16(a.q) && aligned16(a.k) && strides4(a.qs) && strides4(a.ks);
     if (!statistics_only) vec = vec && aligned16(a.v) && aligned16(a.output) && strides4(a.vs) && strides4(a.os);
     if (statistics_only) {
-        if (vec) launch<D, true, true>(a, grid, stream);
-        else launch<D, true, false>(a, grid, stream);
+        if (vec) launch_split<D, true, true>(a, items, stream);
+        else launch_split<D, true, false>(a, items, stream);
     } else {
-        if (vec) launch<D, false, true>(a, grid, stream);
-        else launch<D, false, false>(a, grid, stream);
+        if (vec) launch_split<D, false, true>(a, items, stream);
+        else launch_split<D, false, false>(a, items, stream);
     }
 }
 
@@ -296,9 +307,8 @@ hipError_t launch_forward(const int D, const bool statistics_only, const Forward
     if (tiles > 0x7fffffff || !sequence_fits(a.queries, a.qs, D) || !sequence_fits(a.keys, a.ks, D) ||
             (!statistics_only && !sequence_fits(a.keys, a.vs, D)))
         return hipErrorInvalidValue;
-    const dim3 grid(static_cast<unsigned>(tiles));
-    if (D == 32) dispatch<32>(statistics_only, a, grid, stream);
-    else dispatch<64>(statistics_only, a, grid, stream);
+    if (D == 32) dispatch<32>(statistics_only, a, tiles, stream);
+    else dispatch<64>(statistics_only, a, tiles, stream);
     return hipGetLastError();
 }
 

@@ -33,6 +33,17 @@ inline bool sequence_fits(const int rows, const rocmkernels_strides &s, const in
     return s.token >= 0 && extent * 4 < (1ll << 31);
 }
 
+// Waves per 32-row work item (see WorkItem in attention_device.hpp): split the streamed dimension over 4 waves
+// when there are too few items to give every SIMD of the MI355X (1024) several waves of its own, over 2 for
+// mid-sized grids, not at all for large ones.
+inline int split_for(const long long items) { return items >= 4096 ? 1 : items >= 2048 ? 2 : 4; }
+
+// Workgroups of 4 waves covering `items` items of `split` waves each.
+inline unsigned workgroups_for(const long long items, const int split) {
+    const int per_group = 4 / split;
+    return static_cast<unsigned>((items + per_group - 1) / per_group);
+}
+
 // Forward pass for head width D (32 or 64). statistics_only writes lse and skips V and the output.
 hipError_t launch_forward(int D, bool statistics_only, const ForwardArgs &a, hipStream_t stream);
 
