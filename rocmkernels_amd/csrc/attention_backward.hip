@@ -366,7 +366,7 @@ hipError_t run(const BackwardStage stage, const BackwardArgs &a, hipStream_t str
     const int64_t qitems = static_cast<int64_t>((a.queries + kTile - 1) / kTile) * a.batch * a.heads;
     const int64_t kitems = static_cast<int64_t>((a.keys + kTile - 1) / kTile) * a.batch * a.heads;
     if (stage == kBackwardAll || stage == kBackwardDelta || stage == kBackwardQuery) {
-        const int split = split_for(qitems);
+        const int split = backward_split_for(qitems);
         if (stage == kBackwardDelta) launch_dq<D, kDeltaOnly, VEC, 1>(a, stream);
         else if (stage == kBackwardAll) {
             if (split == 1) launch_dq<D, kDqAndDelta, VEC, 1>(a, stream);
@@ -380,7 +380,7 @@ hipError_t run(const BackwardStage stage, const BackwardArgs &a, hipStream_t str
         const hipError_t error = hipGetLastError();
         if (error != hipSuccess || stage != kBackwardAll) return error;
     }
-    const int split = split_for(kitems);
+    const int split = backward_split_for(kitems);
     if (split == 1) launch_dkdv<D, VEC, 1>(a, stream);
     else if (split == 2) launch_dkdv<D, VEC, 2>(a, stream);
     else launch_dkdv<D, VEC, 4>(a, stream);

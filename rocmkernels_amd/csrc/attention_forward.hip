@@ -280,7 +280,7 @@ void launch(const ForwardArgs &a, const int64_t items, hipStream_t stream) {
 
 template<int D, bool STATS, bool VEC>
 void launch_split(const ForwardArgs &a, const int64_t items, hipStream_t stream) {
-    switch (split_for(items)) {
+    switch (forward_split_for(items)) {
         case 1: launch<D, STATS, VEC, 1>(a, items, stream); break;
         case 2: launch<D, STATS, VEC, 2>(a, items, stream); break;
         default: launch<D, STATS, VEC, 4>(a, items, stream); break;

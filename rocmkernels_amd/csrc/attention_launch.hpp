@@ -34,9 +34,11 @@ inline bool sequence_fits(const int rows, const rocmkernels_strides &s, const in
 }
 
 // Waves per 32-row work item (see WorkItem in attention_device.hpp): split the streamed dimension over 4 waves
-// when there are too few items to give every SIMD of the MI355X (1024) several waves of its own, over 2 for
-// mid-sized grids, not at all for large ones.
-inline int split_for(const long long items) { return items >= 4096 ? 1 : items >= 2048 ? 2 : 4; }
+// when there are too few items to give every SIMD of the MI355X (1024) several waves of its own, not at all for
+// large grids. Measured on MI355X: the forward prefers 4 down to 2048 items; the backward kernels, which hold
+// twice the accumulators and merge them through LDS, prefer 2 there.
+inline int forward_split_for(const long long items) { return items >= 4096 ? 1 : 4; }
+inline int backward_split_for(const long long items) { return items >= 4096 ? 1 : items >= 2048 ? 2 : 4; }
 
 // Workgroups of 4 waves covering `items` items of `split` waves each.
 inline unsigned workgroups_for(const long long items, const int split) {
