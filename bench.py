@@ -150,6 +150,15 @@ def cpu_baseline(seconds):
     }
 
 
+def forward_kernel_name(cfg):
+    """Name rocprofv3 reports for the forward kernel instance that runs on this config: the template arguments are
+    head width, statistics-only, 16-byte vector loads and waves per 32-query item, the last chosen by the item count
+    as rk::forward_split_for (rocmkernels_amd/csrc/attention_launch.hpp) does."""
+    items = (cfg["length"] + 31) // 32 * cfg["batch"] * cfg["heads"]
+    split = 1 if items >= 4096 else 4
+    return f"rk::attention_forward_kernel<{cfg['width']}, false, true, {split}>"
+
+
 def load_traffic(kernel_key):
     path = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(path):
@@ -234,7 +243,7 @@ def main():
     cfg = CONFIGS[args.config]
     measured = measure(cfg, args.steps, args.warmup, backward=not args.no_backward)
     fwd = measured["forward"]
-    kernel = f"attention_forward_kernel<{cfg['width']},false,true>"
+    kernel = forward_kernel_name(cfg)
     result = {
         "metric": METRIC,
         "value": round(fwd["tflops_convention"], 4),
