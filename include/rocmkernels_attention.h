@@ -21,7 +21,10 @@
  *     frees or synchronises, and keeps no state.
  *
  * The *_ex entry points have no counterpart in the reference: they add `int flags` after `radius`, where
- * bit 0 (ROCMKERNELS_ATTENTION_CAUSAL) restricts every query to keys <= query. All other bits must be zero.
+ * bit 0 (ROCMKERNELS_ATTENTION_CAUSAL) restricts every query to keys <= query, and, for the backward only,
+ * bit 1 (ROCMKERNELS_ATTENTION_FUSED_BACKWARD) selects the fused backward: dQ is accumulated with FP32 atomics
+ * inside the dK/dV pass (fewer matrix products, faster), so its low-order bits may differ from run to run;
+ * dK, dV and delta stay bit-reproducible. All other bits must be zero (else hipErrorInvalidValue).
  */
 #ifndef ROCMKERNELS_ATTENTION_H
 #define ROCMKERNELS_ATTENTION_H
@@ -53,6 +56,7 @@ typedef struct rocmkernels_strides {
 } rocmkernels_strides;
 
 #define ROCMKERNELS_ATTENTION_CAUSAL 1
+#define ROCMKERNELS_ATTENTION_FUSED_BACKWARD 2
 
 /* ---- 32-wide forward family ------------------------------------------------------------------ */
 
@@ -142,7 +146,7 @@ ROCMKERNELS_EXPORT int attention_fp32_forward_flash_ex(const float *q, const flo
         float *output, float *lse, int batch, int heads, int queries, int keys, int radius, int flags, rocmkernels_strides qs,
         rocmkernels_strides ks, rocmkernels_strides vs, rocmkernels_strides os, hipStream_t stream);
 
-/* attention_fp32_backward plus flags (bit 0 = causal). */
+/* attention_fp32_backward plus flags (bit 0 = causal, bit 1 = fused backward). */
 ROCMKERNELS_EXPORT int attention_fp32_backward_ex(const float *q, const float *k, const float *v, const bool *mask,
         const float *output, const float *lse, const float *upstream, float *gradient_q, float *gradient_k, float *gradient_v,
         float *delta, int batch, int heads, int queries, int keys, int radius, int flags, rocmkernels_strides qs,
@@ -153,7 +157,7 @@ ROCMKERNELS_EXPORT int attention64_fp32_forward_ex(const float *q, const float *
         float *output, float *lse, int batch, int heads, int queries, int keys, int radius, int flags, rocmkernels_strides qs,
         rocmkernels_strides ks, rocmkernels_strides vs, rocmkernels_strides os, hipStream_t stream);
 
-/* attention64_fp32_backward plus flags (bit 0 = causal). */
+/* attention64_fp32_backward plus flags (bit 0 = causal, bit 1 = fused backward). */
 ROCMKERNELS_EXPORT int attention64_fp32_backward_ex(const float *q, const float *k, const float *v, const bool *mask,
         const float *output, const float *lse, const float *upstream, float *gradient_q, float *gradient_k, float *gradient_v,
         float *delta, int batch, int heads, int queries, int keys, int radius, int flags, rocmkernels_strides qs,

@@ -16,6 +16,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 
 P, I = ctypes.c_void_p, ctypes.c_int
 CAUSAL = 1
+FUSED_BACKWARD = 2
 HIP_ERROR_INVALID_VALUE = 1
 
 
@@ -174,8 +175,12 @@ def statistics(q, k, mask, radius=-1, lse=None, stream=None):
     return lse
 
 
-def backward(q, k, v, mask, output, lse, upstream, radius=-1, causal=False, entry="simple", code=None, grads=None, stream=None):
-    """dQ, dK, dV, delta of attention; gradients packed [B][H][L][D], delta [B][H][Lq]."""
+def backward(q, k, v, mask, output, lse, upstream, radius=-1, causal=False, entry="simple", code=None, grads=None, stream=None,
+             fused=False):
+    """dQ, dK, dV, delta of attention; gradients packed [B][H][L][D], delta [B][H][Lq].
+
+    ``fused`` selects the fused backward of the *_ex entry points (dQ accumulated with atomics: faster, but dQ's
+    low-order bits can change from run to run)."""
     torch = _torch()
     _device_check(q, k, v, mask, output, lse, upstream)
     batch, heads, queries, width = q.shape
@@ -189,9 +194,9 @@ def backward(q, k, v, mask, output, lse, upstream, radius=-1, causal=False, entr
     common = (_ptr(q), _ptr(k), _ptr(v), _ptr(mask), _ptr(output), _ptr(lse), _ptr(upstream), _ptr(gq), _ptr(gk), _ptr(gv),
               _ptr(delta), batch, heads, queries, keys, radius)
     views = (strides(q), strides(k), strides(v), strides(output), strides(upstream), _stream(stream))
-    if causal:
+    if causal or fused:
         name = "attention_fp32_backward_ex" if width == 32 else "attention64_fp32_backward_ex"
-        check(name, *common, CAUSAL, *views)
+        check(name, *common, (CAUSAL if causal else 0) | (FUSED_BACKWARD if fused else 0), *views)
     elif width == 64:
         check("attention64_fp32_backward", *common, *views)
     elif entry in ("tuned", "profile", "query_profile"):

@@ -183,8 +183,8 @@ int attention_fp32_backward_ex(const float *q, const float *k, const float *v, c
         const float *upstream, float *gradient_q, float *gradient_k, float *gradient_v, float *delta, int batch, int heads, int queries,
         int keys, int radius, int flags, rocmkernels_strides qs, rocmkernels_strides ks, rocmkernels_strides vs, rocmkernels_strides os,
         rocmkernels_strides us, hipStream_t stream) {
-    if ((flags & ~ROCMKERNELS_ATTENTION_CAUSAL) != 0 || radius < -1) return kInvalid;
-    return backward(32, flags, rk::kBackwardAll, q, k, v, mask, output, lse, upstream, gradient_q, gradient_k, gradient_v, delta, batch,
+    if ((flags & ~(ROCMKERNELS_ATTENTION_CAUSAL | ROCMKERNELS_ATTENTION_FUSED_BACKWARD)) != 0 || radius < -1) return kInvalid;
+    return backward(32, flags, flags & ROCMKERNELS_ATTENTION_FUSED_BACKWARD ? rk::kBackwardFused : rk::kBackwardAll, q, k, v, mask, output, lse, upstream, gradient_q, gradient_k, gradient_v, delta, batch,
             heads, queries, keys, radius, qs, ks, vs, os, us, stream);
 }
 
@@ -199,8 +199,8 @@ int attention64_fp32_backward_ex(const float *q, const float *k, const float *v,
         const float *upstream, float *gradient_q, float *gradient_k, float *gradient_v, float *delta, int batch, int heads, int queries,
         int keys, int radius, int flags, rocmkernels_strides qs, rocmkernels_strides ks, rocmkernels_strides vs, rocmkernels_strides os,
         rocmkernels_strides us, hipStream_t stream) {
-    if ((flags & ~ROCMKERNELS_ATTENTION_CAUSAL) != 0 || radius < -1) return kInvalid;
-    return backward(64, flags, rk::kBackwardAll, q, k, v, mask, output, lse, upstream, gradient_q, gradient_k, gradient_v, delta, batch,
+    if ((flags & ~(ROCMKERNELS_ATTENTION_CAUSAL | ROCMKERNELS_ATTENTION_FUSED_BACKWARD)) != 0 || radius < -1) return kInvalid;
+    return backward(64, flags, flags & ROCMKERNELS_ATTENTION_FUSED_BACKWARD ? rk::kBackwardFused : rk::kBackwardAll, q, k, v, mask, output, lse, upstream, gradient_q, gradient_k, gradient_v, delta, batch,
             heads, queries, keys, radius, qs, ks, vs, os, us, stream);
 }
 

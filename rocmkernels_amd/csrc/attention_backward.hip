@@ -16,12 +16,17 @@
 // Kernel 2 reads the δ that kernel 1 wrote; they are ordered by the stream, as in the reference
 // (Attention.hip:211-221). Streamed operands are read through buffer resources (see attention_device.hpp), and
 // each tile's row-layout operands are loaded one tile ahead, after the current tile's MFMAs are issued.
+//
+// Fused variant (opt-in, flag ROCMKERNELS_ATTENTION_FUSED_BACKWARD): kernel 1 only computes δ and zeroes dQ;
+// kernel 2 also forms dQ = dS·K/√D for each tile it visits and adds it into dQ with FP32 atomics. That is 5
+// GEMMs per visited tile instead of 7 (kernel 1 no longer recomputes S and dP), at the price of a dQ whose
+// low bits depend on the order in which the atomics land.
 #include "attention_device.hpp"
 #include "attention_launch.hpp"
 
 namespace rk {
 
-enum DqMode { kDqAndDelta = 0, kDeltaOnly = 1, kDqFromDelta = 2 };
+enum DqMode { kDqAndDelta = 0, kDeltaOnly = 1, kDqFromDelta = 2, kDeltaZeroDq = 3 };
 
 template<int D, int MODE, bool VEC, int SPLIT>
 __global__ __launch_bounds__(kThreads) void attention_dq_kernel(const Tensor q, const Tensor k, const Tensor v,
@@ -60,6 +65,21 @@ __global__ __launch_bounds__(kThreads) void attention_dq_kernel(const Tensor q, 
         for (int c = 0; c < HALF; ++c) dlt = fmaf(dor[c], orow[c], dlt);
         dlt = halves_sum(dlt);
         if (w.sub == 0 && h == 0 && qvalid) delta[row] = dlt;
+        if constexpr (MODE == kDeltaZeroDq) {
+            // The fused dK/dV/dQ kernel accumulates into dQ: start every row of this tile at zero.
+            if (qvalid) {
+                float *dst = dq + row * D + h * HALF;
+#pragma unroll
+                for (int c = 0; c < HALF; c += 4) {
+                    if constexpr (VEC) {
+                        *reinterpret_cast<f32x4 *>(dst + c) = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                    } else {
+                        dst[c] = dst[c + 1] = dst[c + 2] = dst[c + 3] = 0.0f;
+                    }
+                }
+            }
+            return;
+        }
         if constexpr (MODE == kDeltaOnly) return;
     }
 
@@ -171,10 +191,10 @@ __global__ __launch_bounds__(kThreads) void attention_dq_kernel(const Tensor q, 
     for (int t = 0; t < DT; ++t) store_tile_row<VEC>(dst + 32 * t, acc[t], scale, h);
 }
 
-template<int D, bool VEC, int SPLIT>
+template<int D, bool VEC, int SPLIT, bool FUSED>
 __global__ __launch_bounds__(kThreads) void attention_dkdv_kernel(const Tensor q, const Tensor k, const Tensor v,
         const uint8_t *__restrict__ mask, const float *__restrict__ lse, const Tensor du, const float *__restrict__ delta,
-        float *__restrict__ dk, float *__restrict__ dv, const Shape s, const float scale) {
+        float *__restrict__ dk, float *__restrict__ dv, float *__restrict__ dq, const Shape s, const float scale) {
     constexpr int HALF = D / 2;
     constexpr int DT = D / 32;
 
@@ -220,6 +240,28 @@ __global__ __launch_bounds__(kThreads) void attention_dkdv_kernel(const Tensor q
     const uint32_t ustep = 4u * du.st;
 
     __shared__ __align__(16) float stats[kWaves][2][kTile];
+
+    // Fused dQ: K of this item in column layout (the B operand of dQ = dS·K, row key0 + tile_row(j, h), feature
+    // 32t + col), pre-scaled by 1/√D and zero for masked keys, whatever K holds there. dS goes through the
+    // wave's LDS slice (row stride kTile + 4 keeps both the row writes and the 128-bit column reads free of
+    // bank conflicts), and dQ rows are added with buffer atomics: rows past the last query fall outside the
+    // resource and are dropped by the hardware.
+    constexpr int KC = FUSED ? DT : 0;
+    float kq[KC > 0 ? KC : 1][16];
+    __shared__ __align__(16) float dsl[FUSED ? kWaves : 1][kTile][kTile + 4];
+    const Buffer qgbuf = make_buffer(dq + static_cast<int64_t>(w.seq) * s.queries * D, FUSED ? static_cast<uint32_t>(s.queries) * (4u * D) : 0u);
+    if constexpr (FUSED) {
+        const uint32_t klane = static_cast<uint32_t>(key0 + 4 * h) * (4u * k.st) + 4u * col;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const bool kept = (bits >> tile_row(j, h)) & 1u;
+#pragma unroll
+            for (int t = 0; t < DT; ++t) {
+                const float x = buffer_load(kbuf, klane + 128u * t, static_cast<uint32_t>(8 * (j >> 2) + (j & 3)) * (4u * k.st));
+                kq[t][j] = kept ? x * scale : 0.0f;
+            }
+        }
+    }
 
     f32x16 acc_k[DT], acc_v[DT];
 #pragma unroll
@@ -309,6 +351,35 @@ __global__ __launch_bounds__(kThreads) void attention_dkdv_kernel(const Tensor q
                 acc_k[t] = mfma(qc[t][j], dp[j], acc_k[t]);
             }
         }
+        if (FUSED && q0 < last) {
+            // dS (keys on lanes) → LDS [query][key] → queries on lanes: A operand of dQ MFMA j is
+            // dS[q0 + col][key0 + tile_row(j, h)], four consecutive keys per 128-bit read.
+#pragma unroll
+            for (int j = 0; j < 16; ++j) dsl[wave][tile_row(j, h)][col] = dp[j];
+            wave_lds_sync();
+            float a[16];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const f32x4 x = *reinterpret_cast<const f32x4 *>(&dsl[wave][col][8 * u + 4 * h]);
+                a[4 * u + 0] = x[0];
+                a[4 * u + 1] = x[1];
+                a[4 * u + 2] = x[2];
+                a[4 * u + 3] = x[3];
+            }
+            wave_lds_sync(); // the next tile overwrites dsl only after these reads
+            const uint32_t qrow = static_cast<uint32_t>(q0 + 4 * h) * (4u * D) + 4u * col;
+#pragma unroll
+            for (int t = 0; t < DT; ++t) {
+                f32x16 acc_q{};
+#pragma unroll
+                for (int j = 0; j < 16; ++j) acc_q = mfma(a[j], kq[t][j], acc_q);
+                // Accumulator register j is row q0 + tile_row(j, h), feature 32t + col.
+#pragma unroll
+                for (int j = 0; j < 16; ++j)
+                    __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(acc_q[j], qgbuf, static_cast<int>(qrow + 128u * t),
+                            static_cast<int>(static_cast<uint32_t>(8 * (j >> 2) + (j & 3)) * (4u * D)), 0);
+            }
+        }
     };
 
     // Tiles sub, sub + SPLIT, ...; the count is rounded up to even so the loop body is two straight-line steps.
@@ -350,14 +421,21 @@ void launch_dq(const BackwardArgs &a, hipStream_t stream) {
             a.lse, tensor(a.upstream, a.us), a.gradient_q, a.delta, shape, scale);
 }
 
-template<int D, bool VEC, int SPLIT>
+template<int D, bool VEC, int SPLIT, bool FUSED>
 void launch_dkdv(const BackwardArgs &a, hipStream_t stream) {
     const Shape shape{a.batch, a.heads, a.queries, a.keys, a.radius, a.causal};
     const float scale = 1.0f / sqrtf(static_cast<float>(D));
     const int64_t items = static_cast<int64_t>((a.keys + kTile - 1) / kTile) * a.batch * a.heads;
-    hipLaunchKernelGGL((attention_dkdv_kernel<D, VEC, SPLIT>), dim3(workgroups_for(items, SPLIT)), dim3(kThreads), 0, stream, tensor(a.q, a.qs),
-            tensor(a.k, a.ks), tensor(a.v, a.vs), reinterpret_cast<const uint8_t *>(a.mask), a.lse, tensor(a.upstream, a.us), a.delta,
-            a.gradient_k, a.gradient_v, shape, scale);
+    hipLaunchKernelGGL((attention_dkdv_kernel<D, VEC, SPLIT, FUSED>), dim3(workgroups_for(items, SPLIT)), dim3(kThreads), 0, stream,
+            tensor(a.q, a.qs), tensor(a.k, a.ks), tensor(a.v, a.vs), reinterpret_cast<const uint8_t *>(a.mask), a.lse,
+            tensor(a.upstream, a.us), a.delta, a.gradient_k, a.gradient_v, a.gradient_q, shape, scale);
+}
+
+template<int D, bool VEC, bool FUSED>
+void launch_dkdv_split(const BackwardArgs &a, const int split, hipStream_t stream) {
+    if (split == 1) launch_dkdv<D, VEC, 1, FUSED>(a, stream);
+    else if (split == 2) launch_dkdv<D, VEC, 2, FUSED>(a, stream);
+    else launch_dkdv<D, VEC, 4, FUSED>(a, stream);
 }
 
 
@@ -365,6 +443,13 @@ template<int D, bool VEC>
 hipError_t run(const BackwardStage stage, const BackwardArgs &a, hipStream_t stream) {
     const int64_t qitems = static_cast<int64_t>((a.queries + kTile - 1) / kTile) * a.batch * a.heads;
     const int64_t kitems = static_cast<int64_t>((a.keys + kTile - 1) / kTile) * a.batch * a.heads;
+    if (stage == kBackwardFused) {
+        launch_dq<D, kDeltaZeroDq, VEC, 1>(a, stream);
+        const hipError_t error = hipGetLastError();
+        if (error != hipSuccess) return error;
+        launch_dkdv_split<D, VEC, true>(a, backward_split_for(kitems), stream);
+        return hipGetLastError();
+    }
     if (stage == kBackwardAll || stage == kBackwardDelta || stage == kBackwardQuery) {
         const int split = backward_split_for(qitems);
         if (stage == kBackwardDelta) launch_dq<D, kDeltaOnly, VEC, 1>(a, stream);
@@ -380,10 +465,7 @@ hipError_t run(const BackwardStage stage, const BackwardArgs &a, hipStream_t str
         const hipError_t error = hipGetLastError();
         if (error != hipSuccess || stage != kBackwardAll) return error;
     }
-    const int split = backward_split_for(kitems);
-    if (split == 1) launch_dkdv<D, VEC, 1>(a, stream);
-    else if (split == 2) launch_dkdv<D, VEC, 2>(a, stream);
-    else launch_dkdv<D, VEC, 4>(a, stream);
+    launch_dkdv_split<D, VEC, false>(a, backward_split_for(kitems), stream);
     return hipGetLastError();
 }
 
@@ -395,6 +477,7 @@ hipError_t launch_backward(const int D, const BackwardStage stage, const Backwar
     if (qblocks > 0x7fffffff || kblocks > 0x7fffffff || !sequence_fits(a.queries, a.qs, D) || !sequence_fits(a.keys, a.ks, D) ||
             !sequence_fits(a.keys, a.vs, D) || !sequence_fits(a.queries, a.os, D) || !sequence_fits(a.queries, a.us, D))
         return hipErrorInvalidValue;
+    if (stage == kBackwardFused && !sequence_fits(a.queries, rocmkernels_strides{0, 0, D}, D)) return hipErrorInvalidValue; // packed dQ, atomics
     const bool vec = aligned16(a.q) && aligned16(a.k) && aligned16(a.v) && aligned16(a.output) && aligned16(a.upstream) &&
             aligned16(a.gradient_q) && aligned16(a.gradient_k) && aligned16(a.gradient_v) && strides4(a.qs) && strides4(a.ks) &&
             strides4(a.vs) && strides4(a.os) && strides4(a.us);

@@ -54,6 +54,7 @@ enum BackwardStage {
     kBackwardDelta = 1,  // delta only
     kBackwardQuery = 2,  // dQ only, reading delta
     kBackwardKeyValue = 3, // dK/dV only, reading delta
+    kBackwardFused = 4,    // delta and dQ = 0, then dK/dV with dQ accumulated by atomics (not bit-reproducible)
 };
 
 hipError_t launch_backward(int D, BackwardStage stage, const BackwardArgs &a, hipStream_t stream);

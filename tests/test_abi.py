@@ -87,6 +87,9 @@ BWD_OK = lambda: [_buf()] * 11  # noqa: E731
     ("attention_fp32_forward_flash_ex", FWD_OK() + [1, 1, 1, 1, -1, 2, S0, S0, S0, S0, None]),
     ("attention_fp32_forward_flash_ex", FWD_OK() + [1, 1, 1, 1, -7, 1, S0, S0, S0, S0, None]),
     ("attention_fp32_backward_ex", BWD_OK() + [1, 1, 1, 1, -1, 4, S0, S0, S0, S0, S0, None]),
+    ("attention_fp32_backward_ex", BWD_OK() + [1, 1, 0, 1, -1, 3, S0, S0, S0, S0, S0, None]),
+    ("attention64_fp32_backward_ex", BWD_OK()[:7] + [None] + BWD_OK()[8:] + [1, 1, 1, 1, -1, 2, S0, S0, S0, S0, S0, None]),
+    ("attention64_fp32_forward_ex", FWD_OK() + [1, 1, 1, 1, -1, 2, S0, S0, S0, S0, None]),
     ("attention64_fp32_forward_ex", FWD_OK()[:3] + [None] + FWD_OK()[4:] + [1, 1, 1, 1, -1, 1, S0, S0, S0, S0, None]),
     ("attention64_fp32_backward_ex", BWD_OK() + [1, 1, 1, 1, -1, -1, S0, S0, S0, S0, S0, None]),
 ])

@@ -370,3 +370,65 @@ def test_results_are_deterministic(device):
     second = run_both(device, q, k, v, du, mask, causal=True)
     for a, b in zip(first, second):
         assert np.array_equal(a, b, equal_nan=True)
+
+
+# ---- fused backward (flag ROCMKERNELS_ATTENTION_FUSED_BACKWARD of the *_ex entry points) -----------------------
+
+def run_fused_and_default(device, q, k, v, du, mask, radius, causal):
+    tq, tk, tv, tdu, tm = to_dev(device, q, k, v, du, mask)
+    out, lse = attention.forward(tq, tk, tv, tm, radius=radius, causal=causal)
+    fused = attention.backward(tq, tk, tv, tm, out, lse, tdu, radius=radius, causal=causal, fused=True)
+    default = attention.backward(tq, tk, tv, tm, out, lse, tdu, radius=radius, causal=causal)
+    return host(out, lse, *fused), host(*default)
+
+
+@pytest.mark.parametrize("width,batch,heads,queries,keys,radius,causal,pad", [
+    (32, 2, 3, 100, 100, -1, True, True),
+    (32, 1, 2, 50, 90, -1, False, True),
+    (32, 1, 2, 90, 50, 11, True, True),
+    (32, 3, 1, 33, 33, 0, False, False),
+    (32, 1, 1, 1, 70, -1, False, True),
+    (32, 2, 2, 256, 256, -1, True, False),
+    (64, 2, 2, 130, 130, 17, True, True),
+    (64, 1, 2, 90, 50, -1, False, True),
+    (64, 2, 1, 64, 200, -1, True, False),
+    (64, 1, 3, 5, 7, 2, False, False),
+])
+def test_fused_backward_matches_oracle(device, width, batch, heads, queries, keys, radius, causal, pad):
+    q, k, v, du = normal_case(700 + queries + keys, width, batch, heads, queries, keys)
+    mask = padding_mask(705, batch, keys, max(1, keys // 2)) if pad else np.ones((batch, keys), np.uint8)
+    want = oracle.attention(q, k, v, mask, du, radius=radius, causal=causal)
+    (out, lse, gq, gk, gv, delta), (_, dk, dv, ddelta) = run_fused_and_default(device, q, k, v, du, mask, radius, causal)
+    check_forward(out, lse, want)
+    check_backward(gq, gk, gv, delta, want, "fused")
+    # dK, dV and delta come from the same arithmetic as the default backward: bit-identical.
+    assert np.array_equal(gk.view(np.int32), dk.view(np.int32))
+    assert np.array_equal(gv.view(np.int32), dv.view(np.int32))
+    assert np.array_equal(delta.view(np.int32), ddelta.view(np.int32))
+
+
+def test_fused_backward_config3_and_masked_batch(device):
+    # Config 3 in full (B2 x H12 x 1024 x 32 causal), with batch 1's keys 0..99 masked and holding NaN: masked
+    # keys must not reach dQ through the atomics.
+    shape = (2, 12, 1024, 32)
+    q, k, v, du = (inputs.normal(seed, shape) for seed in (101, 102, 103, 104))
+    mask = np.ones((2, 1024), np.uint8)
+    mask[1, :100] = 0
+    k[1, :, :100] = np.nan
+    v[1, :, :100] = np.nan
+    want = oracle.attention(q, k, v, mask, du, causal=True)
+    (out, lse, gq, gk, gv, delta), _ = run_fused_and_default(device, q, k, v, du, mask, -1, True)
+    assert np.all(np.isfinite(gq))
+    check_forward(np.nan_to_num(out), lse, {**want, "output": np.nan_to_num(want["output"])}, "config 3 fused")
+    check_backward(gq, gk, gv, delta, want, "config 3 fused")
+
+
+def test_fused_backward_config4_subset(device):
+    lengths = inputs.uniform_int(105, 32, 1024, 2048)
+    mask = (np.arange(2048)[None, :] < lengths[:, None]).astype(np.uint8)
+    q, k, v, du = baseline_inputs(64, 32, 2048)
+    (out, lse, gq, gk, gv, delta), _ = run_fused_and_default(device, q, k, v, du, mask, -1, True)
+    part = slice(0, 3)
+    want = oracle.attention(q[part], k[part], v[part], mask[part], du[part], causal=True)
+    check_backward(gq[part], gk[part], gv[part], delta[part], want, "config 4 fused")
+    assert np.all(np.isfinite(gq))
