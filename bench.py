@@ -153,13 +153,18 @@ def cpu_baseline(seconds):
     }
 
 
-def forward_kernel_name(cfg):
-    """Name rocprofv3 reports for the forward kernel instance that runs on this config: the template arguments are
-    head width, statistics-only, 16-byte vector loads and waves per 32-query item, the last chosen by the item count
-    as rk::forward_split_for (rocmkernels_amd/csrc/attention_launch.hpp) does."""
+def forward_kernel_name(cfg, cus):
+    """Name rocprofv3 reports for the forward kernel instance that runs on this config. Template arguments: head width,
+    statistics-only, 16-byte vector loads, waves per 32-query item and items per persistent workgroup (0: dispatch
+    order), chosen from the item count as rk::launch_mapped (rocmkernels_amd/csrc/attention_forward.hip) does."""
     items = (cfg["length"] + 31) // 32 * cfg["batch"] * cfg["heads"]
+    resident = 3 if cfg["width"] == 32 else 2
+    if cus < items <= resident * cus:
+        bins = min(items, cus)
+        rounds = -(-items // bins)
+        return f"rk::attention_forward_kernel<{cfg['width']}, false, true, 4, {3 if rounds == 3 else 2}>"
     split = 1 if items >= 4096 else 4
-    return f"rk::attention_forward_kernel<{cfg['width']}, false, true, {split}>"
+    return f"rk::attention_forward_kernel<{cfg['width']}, false, true, {split}, 0>"
 
 
 def load_traffic(kernel_key):
@@ -256,7 +261,7 @@ def main():
     cfg = CONFIGS[args.config]
     measured = measure(cfg, args.steps, args.warmup, backward=not args.no_backward)
     fwd = measured["forward"]
-    kernel = forward_kernel_name(cfg)
+    kernel = forward_kernel_name(cfg, torch.cuda.get_device_properties(0).multi_processor_count)
     result = {
         "metric": METRIC,
         "value": round(fwd["tflops_convention"], 4),

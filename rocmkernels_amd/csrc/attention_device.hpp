@@ -19,6 +19,8 @@
 
 #include <stdint.h>
 
+#include "attention_plan.hpp"
+
 namespace rk {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -196,6 +198,7 @@ __device__ __forceinline__ int window_query_hi(const Shape &s, const int key) { 
 // 8 consecutive workgroups of one rank spread over the 8 XCDs while each XCD keeps a fixed subset of sequences.
 struct WorkItem {
     int seq, b, head, rank, sub;
+    int split; // waves sharing the item
     bool valid;
 };
 
@@ -206,9 +209,30 @@ __device__ __forceinline__ WorkItem work_item(const Shape &s, const int tiles_pe
     const int item = blockIdx.x * (kWaves / SPLIT) + wave / SPLIT;
     WorkItem w;
     w.sub = wave % SPLIT;
+    w.split = SPLIT;
     w.valid = item < seqs * tiles_per_seq;
     w.rank = item / seqs;
     w.seq = item - w.rank * seqs;
+    w.b = w.seq / s.heads;
+    w.head = w.seq - w.b * s.heads;
+    return w;
+}
+
+// Planned mapping (persistent grid, see attention_plan.hpp): the NI * SPLIT waves of workgroup blockIdx.x take the NI
+// items of its bin, item i on waves i*SPLIT .. i*SPLIT + SPLIT - 1. Waves are dealt to the 4 SIMDs round-robin, so with
+// SPLIT = 4 every SIMD runs one quarter of every item of the bin and carries a quarter of the bin's cost-balanced load.
+template<int SPLIT>
+__device__ __forceinline__ WorkItem planned_item(const Shape &s, const Plan &plan) {
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave); // wave-uniform: keeps tile bookkeeping scalar
+    const int group = static_cast<int>(blockIdx.x) % plan.groups;
+    const int bin = static_cast<int>(blockIdx.x) / plan.groups;
+    const int p = plan_position(plan, bin, wave / SPLIT);
+    WorkItem w;
+    w.sub = wave % SPLIT;
+    w.split = SPLIT;
+    w.valid = p < plan.seqs * plan.tiles;
+    w.rank = w.valid ? p / plan.seqs : 0;
+    w.seq = group + plan.groups * (w.valid ? p - w.rank * plan.seqs : 0);
     w.b = w.seq / s.heads;
     w.head = w.seq - w.b * s.heads;
     return w;

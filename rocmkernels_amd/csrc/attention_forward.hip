@@ -5,29 +5,34 @@
 // the statistics-only instance (Attention.hip:252-261) and attention64_query<false> (Attention64.hip:34-129).
 // The maths is the same (O = softmax(QKᵀ/√D + mask) V with lse = {max, Σexp(s - max)}); the mapping is not:
 //
-//   * A workgroup owns one 32-query tile of one (batch, head) and runs 4 waves, one per SIMD. The waves split
-//     the 32-key tiles of the query tile's key range round-robin, each keeping its own online-softmax state
-//     (m, l, Oᵀ), and merge once through LDS at the end. That bounds the longest workgroup to a quarter of a
-//     row, which matters at the causal 24x1024 shape where rows are short and the grid is small.
+//   * A work item is one 32-query tile of one (batch, head). SPLIT waves (1, 2 or 4, one per SIMD) split the 32-key
+//     tiles of its key range round-robin, each keeping its own online-softmax state (m, l, Oᵀ), and merge once
+//     through LDS at the end. With few items (the causal 24x1024 shape has 768, under one per SIMD) the grid is
+//     persistent: one workgroup per CU takes a bin of 2 or 3 items chosen so that every bin costs the same number
+//     of key tiles (attention_plan.hpp), 4 waves per item; otherwise items go to 4-wave workgroups in dispatch
+//     order and the hardware balances them.
 //   * Sᵀ = K·Qᵀ and Oᵀ += Vᵀ·Pᵀ run on v_mfma_f32_32x32x2f32; the Sᵀ accumulator register j is the B operand
 //     of Oᵀ MFMA j, so P never leaves registers. Each lane owns one query, so the row maximum is 15 VALU max
 //     plus one exchange with the other half-wave, and the rescale of Oᵀ is lane-local.
 //   * exp(s - m) is evaluated as exp2(s·(log2e/√D) - m·(log2e/√D)) with one FMA feeding v_exp_f32.
-//   * blockIdx → work: the heaviest query tiles (the last ones under a causal mask) are dispatched first, and
-//     consecutive workgroups take consecutive (batch, head) pairs of the same tile, so with B·H a multiple of 8
-//     each XCD keeps a fixed subset of sequences in its own L2.
+//   * blockIdx → work: in dispatch order the heaviest query tiles (the last ones under a causal mask) go first, and
+//     consecutive workgroups take consecutive (batch, head) pairs of the same tile; in both mappings, with B·H a
+//     multiple of 8, each XCD (workgroup index mod 8) keeps a fixed subset of sequences in its own L2.
 #include "attention_device.hpp"
 #include "attention_launch.hpp"
 
 namespace rk {
 
-template<int D, bool STATS, bool VEC, int SPLIT>
-__global__ __launch_bounds__(kThreads) void attention_forward_kernel(const Tensor q, const Tensor k, const Tensor v,
-        const uint8_t *__restrict__ mask, float *__restrict__ out, const int osb, const int osh, const int ost,
-        float *__restrict__ lse, const Shape s, const float scale) {
+// NI = 0: one work item per SPLIT waves of 4-wave workgroups, in dispatch order (work_item). NI > 0: persistent grid
+// of NI * SPLIT-wave workgroups, each taking the NI items of its bin of `plan` (planned_item).
+template<int D, bool STATS, bool VEC, int SPLIT, int NI>
+__global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attention_forward_kernel(const Tensor q, const Tensor k,
+        const Tensor v, const uint8_t *__restrict__ mask, float *__restrict__ out, const int osb, const int osh, const int ost,
+        float *__restrict__ lse, const Shape s, const Plan plan, const float scale) {
     constexpr int HALF = D / 2; // features per lane in row layout
     constexpr int DT = D / 32;  // 32-feature slices of the output
     constexpr int NREG = STATS ? 0 : 16 * DT;
+    constexpr int WG = NI > 0 ? NI * SPLIT : kWaves; // waves per workgroup
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave); // wave-uniform: keeps tile bookkeeping scalar
@@ -35,8 +40,9 @@ __global__ __launch_bounds__(kThreads) void attention_forward_kernel(const Tenso
     const int h = lane >> 5;
 
     const int qtiles = (s.queries + kTile - 1) / kTile;
-    const WorkItem w = work_item<SPLIT>(s, qtiles);
+    const WorkItem w = NI > 0 ? planned_item<SPLIT>(s, plan) : work_item<SPLIT>(s, qtiles);
     const int seq = w.seq, b = w.b, head = w.head, sub = w.sub;
+    constexpr int split = SPLIT; // waves sharing this item
     const int qt = s.causal ? qtiles - 1 - w.rank : w.rank;
     const int q0 = qt * kTile;
     const int query = q0 + col;
@@ -175,26 +181,26 @@ __global__ __launch_bounds__(kThreads) void attention_forward_kernel(const Tenso
         }
     };
 
-    // The wave visits tiles sub, sub + SPLIT, ...; their count is rounded up to even so the loop body is two
+    // The wave visits tiles sub, sub + split, ...; their count is rounded up to even so the loop body is two
     // straight-line steps (the padding step sees no key).
-    const int mine = ntiles > sub ? (ntiles - sub + SPLIT - 1) / SPLIT : 0;
+    const int mine = ntiles > sub ? (ntiles - sub + split - 1) / split : 0;
     Tile ta, tb;
     if (mine > 0) load_tile(ta, first + sub * kTile);
     for (int i = 0; i < mine; i += 2) {
-        const int key0 = first + (sub + i * SPLIT) * kTile;
-        step(ta, key0, tb, key0 + SPLIT * kTile);
-        step(tb, key0 + SPLIT * kTile, ta, key0 + 2 * SPLIT * kTile);
+        const int key0 = first + (sub + i * split) * kTile;
+        step(ta, key0, tb, key0 + split * kTile);
+        step(tb, key0 + split * kTile, ta, key0 + 2 * split * kTile);
     }
     const float mc_run = mc; // offset the wave's (l_run, o) are expressed against
 
-    // Merge the states of the SPLIT waves of the item: waves with sub > 0 publish (m, l, mc, Oᵀ) in LDS, the
+    // Merge the states of the `split` waves of the item: waves with sub > 0 publish (m, l, mc, Oᵀ) in LDS, the
     // wave with sub == 0 combines. Every state satisfies l_w = Σ exp2(s·c2 - mc_w); they are combined against the
     // largest offset, and lse's sum is then expressed against the true maximum.
     float m_all = m_run;
     float mc_all = mc_run;
     float base = 0.0f, l_all = l_run;
     if constexpr (SPLIT > 1) {
-        __shared__ float partial[kWaves][NREG + 3][kWave];
+        __shared__ float partial[WG][NREG + 3][kWave];
         if (sub > 0) {
             partial[wave][0][lane] = m_run;
             partial[wave][1][lane] = l_run;
@@ -210,7 +216,7 @@ __global__ __launch_bounds__(kThreads) void attention_forward_kernel(const Tenso
         __syncthreads();
         if (sub != 0) return;
 #pragma unroll
-        for (int x = 1; x < SPLIT; ++x) {
+        for (int x = 1; x < split; ++x) {
             m_all = fmaxf(m_all, partial[wave + x][0][lane]);
             mc_all = fmaxf(mc_all, partial[wave + x][2 + NREG][lane]);
         }
@@ -222,7 +228,7 @@ __global__ __launch_bounds__(kThreads) void attention_forward_kernel(const Tenso
             for (int t = 0; t < DT; ++t) o[t] *= a0;
         }
 #pragma unroll
-        for (int x = 1; x < SPLIT; ++x) {
+        for (int x = 1; x < split; ++x) {
             const float aw = exp2_fast(partial[wave + x][2 + NREG][lane] - base);
             l_all = fmaf(partial[wave + x][1][lane], aw, l_all);
             if constexpr (!STATS) {
@@ -268,35 +274,59 @@ namespace {
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 bool strides4(const rocmkernels_strides &s) { return ((s.batch | s.head | s.token) & 3) == 0; }
 
-template<int D, bool STATS, bool VEC, int SPLIT>
-void launch(const ForwardArgs &a, const int64_t items, hipStream_t stream) {
+template<int D, bool STATS, bool VEC, int SPLIT, int NI>
+void launch(const ForwardArgs &a, const int64_t items, const Plan &plan, hipStream_t stream) {
     const Shape shape{a.batch, a.heads, a.queries, a.keys, a.radius, a.causal};
     const float scale = 1.0f / sqrtf(static_cast<float>(D));
-    hipLaunchKernelGGL((attention_forward_kernel<D, STATS, VEC, SPLIT>), dim3(workgroups_for(items, SPLIT)), dim3(kThreads),
-            0, stream, Tensor{a.q, a.qs.batch, a.qs.head, a.qs.token}, Tensor{a.k, a.ks.batch, a.ks.head, a.ks.token},
+    const unsigned grid = NI > 0 ? static_cast<unsigned>(plan.groups * plan.bins) : workgroups_for(items, SPLIT);
+    const unsigned threads = kWave * (NI > 0 ? NI * SPLIT : kWaves);
+    hipLaunchKernelGGL((attention_forward_kernel<D, STATS, VEC, SPLIT, NI>), dim3(grid), dim3(threads), 0, stream,
+            Tensor{a.q, a.qs.batch, a.qs.head, a.qs.token}, Tensor{a.k, a.ks.batch, a.ks.head, a.ks.token},
             Tensor{a.v, a.vs.batch, a.vs.head, a.vs.token}, reinterpret_cast<const uint8_t *>(a.mask), a.output, a.os.batch,
-            a.os.head, a.os.token, a.lse, shape, scale);
+            a.os.head, a.os.token, a.lse, shape, plan, scale);
 }
 
+// Items (32-query tiles) of 4 waves each that one CU runs at once: 3 at d=32 (about 155 VGPRs per wave), 2 at d=64
+// (about 250).
+template<int D>
+constexpr int resident_items_per_cu() { return D == 32 ? 3 : 2; }
+
 template<int D, bool STATS, bool VEC>
-void launch_split(const ForwardArgs &a, const int64_t items, hipStream_t stream) {
+void launch_mapped(const ForwardArgs &a, const int64_t items, const int cus, hipStream_t stream) {
+    if (items > cus && items <= static_cast<int64_t>(resident_items_per_cu<D>()) * cus) {
+        // Every CU holds its whole bin at once: one persistent workgroup per CU takes a cost-balanced bin of items (the
+        // causal mask makes item costs range from 1 to L/32 tiles), each item on 4 waves, one per SIMD, so that every
+        // SIMD carries a quarter of the bin.
+        const int qtiles = (a.queries + kTile - 1) / kTile;
+        const Plan plan = make_plan(static_cast<int64_t>(a.batch) * a.heads, qtiles, cus, a.causal != 0);
+        if constexpr (resident_items_per_cu<D>() >= 3) {
+            if (plan.rounds == 3) {
+                launch<D, STATS, VEC, 4, 3>(a, items, plan, stream);
+                return;
+            }
+        }
+        launch<D, STATS, VEC, 4, 2>(a, items, plan, stream);
+        return;
+    }
+    // Otherwise one item per 1, 2 or 4 waves of 4-wave workgroups, heaviest first, left to the hardware dispatcher.
+    const Plan none{1, 1, 1, 1, 1, 0};
     switch (forward_split_for(items)) {
-        case 1: launch<D, STATS, VEC, 1>(a, items, stream); break;
-        case 2: launch<D, STATS, VEC, 2>(a, items, stream); break;
-        default: launch<D, STATS, VEC, 4>(a, items, stream); break;
+        case 1: launch<D, STATS, VEC, 1, 0>(a, items, none, stream); break;
+        case 2: launch<D, STATS, VEC, 2, 0>(a, items, none, stream); break;
+        default: launch<D, STATS, VEC, 4, 0>(a, items, none, stream); break;
     }
 }
 
 template<int D>
-void dispatch(const bool statistics_only, const ForwardArgs &a, const int64_t items, hipStream_t stream) {
+void dispatch(const bool statistics_only, const ForwardArgs &a, const int64_t items, const int cus, hipStream_t stream) {
     bool vec = aligned16(a.q) && aligned16(a.k) && strides4(a.qs) && strides4(a.ks);
     if (!statistics_only) vec = vec && aligned16(a.v) && aligned16(a.output) && strides4(a.vs) && strides4(a.os);
     if (statistics_only) {
-        if (vec) launch_split<D, true, true>(a, items, stream);
-        else launch_split<D, true, false>(a, items, stream);
+        if (vec) launch_mapped<D, true, true>(a, items, cus, stream);
+        else launch_mapped<D, true, false>(a, items, cus, stream);
     } else {
-        if (vec) launch_split<D, false, true>(a, items, stream);
-        else launch_split<D, false, false>(a, items, stream);
+        if (vec) launch_mapped<D, false, true>(a, items, cus, stream);
+        else launch_mapped<D, false, false>(a, items, cus, stream);
     }
 }
 
@@ -307,8 +337,11 @@ hipError_t launch_forward(const int D, const bool statistics_only, const Forward
     if (tiles > 0x7fffffff || !sequence_fits(a.queries, a.qs, D) || !sequence_fits(a.keys, a.ks, D) ||
             (!statistics_only && !sequence_fits(a.keys, a.vs, D)))
         return hipErrorInvalidValue;
-    if (D == 32) dispatch<32>(statistics_only, a, tiles, stream);
-    else dispatch<64>(statistics_only, a, tiles, stream);
+    int cus = 0;
+    const hipError_t error = compute_units(cus);
+    if (error != hipSuccess) return error;
+    if (D == 32) dispatch<32>(statistics_only, a, tiles, cus, stream);
+    else dispatch<64>(statistics_only, a, tiles, cus, stream);
     return hipGetLastError();
 }
 

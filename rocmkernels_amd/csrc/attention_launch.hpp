@@ -40,6 +40,14 @@ inline bool sequence_fits(const int rows, const rocmkernels_strides &s, const in
 inline int forward_split_for(const long long items) { return items >= 4096 ? 1 : 4; }
 inline int backward_split_for(const long long items) { return items >= 4096 ? 1 : items >= 2048 ? 2 : 4; }
 
+// Compute units of the current device (256 on MI355X).
+inline hipError_t compute_units(int &cus) {
+    int device = 0;
+    const hipError_t error = hipGetDevice(&device);
+    if (error != hipSuccess) return error;
+    return hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+}
+
 // Workgroups of 4 waves covering `items` items of `split` waves each.
 inline unsigned workgroups_for(const long long items, const int split) {
     const int per_group = 4 / split;

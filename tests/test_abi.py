@@ -118,3 +118,14 @@ def test_cpp_wrappers_throw_hip_error(tmp_path):
                               ["-std=c++17", "-Wall", "-Wextra", "-Werror", "-D__HIP_PLATFORM_AMD__"])
     assert result.returncode == 0, result.stdout + result.stderr
     assert "0 failure(s)" in result.stdout
+
+
+def test_persistent_work_partition_deals_every_item_once_and_balances(tmp_path):
+    binary = str(tmp_path / "plan_check")
+    source = os.path.join(ROOT, "tests", "cpp", "plan_check.cpp")
+    csrc = os.path.join(ROOT, "rocmkernels_amd", "csrc")
+    subprocess.run(["g++", "-std=c++17", "-Wall", "-Wextra", "-Werror", "-D__HIP_PLATFORM_AMD__", f"-I{csrc}",
+                    "-I/opt/rocm/include", source, "-o", binary], check=True, capture_output=True, text=True)
+    result = subprocess.run([binary], capture_output=True, text=True, timeout=60)
+    assert result.returncode == 0, result.stdout + result.stderr
+    assert "0 failure(s)" in result.stdout
