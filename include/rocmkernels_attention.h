@@ -163,6 +163,23 @@ ROCMKERNELS_EXPORT int attention64_fp32_backward_ex(const float *q, const float 
         float *delta, int batch, int heads, int queries, int keys, int radius, int flags, rocmkernels_strides qs,
         rocmkernels_strides ks, rocmkernels_strides vs, rocmkernels_strides os, rocmkernels_strides us, hipStream_t stream);
 
+/* ---- generic forward (16-, 32- or 64-wide heads, fp32 or fp16 storage) --------------------------------- */
+
+/* Storage type of attention_generic_forward's q, k, v and output; accumulation is always fp32 (reference:
+ * ROCmKernels.Kernels/include/ROCmKernels/Kernels/DType.hpp:7-8, `enum class DType : unsigned char { Float32, Float16 }`). */
+typedef unsigned char rocmkernels_dtype;
+#define ROCMKERNELS_DTYPE_FLOAT32 0
+#define ROCMKERNELS_DTYPE_FLOAT16 1
+
+/* Replaces attention_generic_forward (reference Generic/AttentionGeneric.hpp:10-13,
+ * Generic/Attention/AttentionGeneric.hip:291-309): windowed forward for headWidth 16, 32 or 64 with q, k, v and
+ * output of type dtype (fp32 lse). No causal mask. hipErrorInvalidValue for null pointers, non-positive sizes,
+ * radius < -1, another headWidth or an unknown dtype. fp16 rows are read with 128-bit loads when every pointer is
+ * 16-byte aligned and every stride a multiple of 8 elements. */
+ROCMKERNELS_EXPORT int attention_generic_forward(const void *q, const void *k, const void *v, const bool *mask, void *output,
+        float *lse, int batch, int heads, int queries, int keys, int headWidth, int radius, rocmkernels_strides qs,
+        rocmkernels_strides ks, rocmkernels_strides vs, rocmkernels_strides os, rocmkernels_dtype dtype, hipStream_t stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

@@ -17,6 +17,8 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 P, I = ctypes.c_void_p, ctypes.c_int
 CAUSAL = 1
 FUSED_BACKWARD = 2
+DTYPE_FLOAT32 = 0  # rocmkernels_dtype / ROCmKernels::Kernels::DType::Float32
+DTYPE_FLOAT16 = 1
 HIP_ERROR_INVALID_VALUE = 1
 
 
@@ -50,6 +52,7 @@ ENTRY_POINTS = {
     "attention_fp32_backward_ex": _BACKWARD_CODE,
     "attention64_fp32_forward_ex": _FORWARD_CODE,
     "attention64_fp32_backward_ex": _BACKWARD_CODE,
+    "attention_generic_forward": [P, P, P, P, P, P, I, I, I, I, I, I, S, S, S, S, ctypes.c_ubyte, P],
 }
 
 _lib = None
@@ -118,7 +121,7 @@ def _device_check(*tensors):
     for t in tensors:
         if t is not None and not t.is_cuda:
             raise ValueError("the attention kernels run on the GPU only; move the tensor to a HIP device")
-        if t is not None and t.dtype not in (_torch().float32, _torch().bool, _torch().uint8):
+        if t is not None and t.dtype not in (_torch().float32, _torch().float16, _torch().bool, _torch().uint8):
             raise ValueError(f"unsupported dtype {t.dtype}")
 
 
@@ -160,6 +163,24 @@ def forward(q, k, v, mask, radius=-1, causal=False, output=None, lse=None, entry
         check("attention_fp32_forward_tuned" if entry == "tuned" else "attention_fp32_forward_flash_tuned", *common, code, *views)
     else:
         check(_FORWARD_NAMES[(entry if width == 32 else "simple", width)], *common, *views)
+    return output, lse
+
+
+def generic_forward(q, k, v, mask, radius=-1, output=None, lse=None, stream=None):
+    """attention_generic_forward: q/k/v [B][H][L][D] float32 or float16 views (D = 16, 32 or 64) on the GPU, mask
+    [B][keys]. Returns (output, lse): output has q's dtype, lse is float32 [B][H][Lq][2]."""
+    torch = _torch()
+    _device_check(q, k, v, mask)
+    if not (q.dtype == k.dtype == v.dtype) or q.dtype not in (torch.float32, torch.float16):
+        raise ValueError("q, k and v must all be float32 or all float16")
+    batch, heads, queries, width = q.shape
+    if output is None:
+        output = torch.empty((batch, heads, queries, width), device=q.device, dtype=q.dtype)
+    if lse is None:
+        lse = torch.empty((batch, heads, queries, 2), device=q.device, dtype=torch.float32)
+    dtype = DTYPE_FLOAT16 if q.dtype == torch.float16 else DTYPE_FLOAT32
+    check("attention_generic_forward", _ptr(q), _ptr(k), _ptr(v), _ptr(mask), _ptr(output), _ptr(lse), batch, heads, queries,
+          k.shape[2], width, radius, strides(q), strides(k), strides(v), strides(output), dtype, _stream(stream))
     return output, lse
 
 

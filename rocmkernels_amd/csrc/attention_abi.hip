@@ -204,4 +204,23 @@ int attention64_fp32_backward_ex(const float *q, const float *k, const float *v,
             heads, queries, keys, radius, qs, ks, vs, os, us, stream);
 }
 
+// Reference Generic/Attention/AttentionGeneric.hip:291-309.
+int attention_generic_forward(const void *q, const void *k, const void *v, const bool *mask, void *output, float *lse, int batch, int heads,
+        int queries, int keys, int headWidth, int radius, rocmkernels_strides qs, rocmkernels_strides ks, rocmkernels_strides vs,
+        rocmkernels_strides os, rocmkernels_dtype dtype, hipStream_t stream) {
+    if (!q || !k || !v || !mask || !output || !lse || bad_dims(batch, heads, queries, keys)) return kInvalid;
+    if (headWidth != 16 && headWidth != 32 && headWidth != 64) return kInvalid;
+    if (radius < -1) return kInvalid;
+    if (dtype == ROCMKERNELS_DTYPE_FLOAT32) {
+        const ForwardArgs a{static_cast<const float *>(q), static_cast<const float *>(k), static_cast<const float *>(v), mask,
+                static_cast<float *>(output), lse, batch, heads, queries, keys, radius, 0, qs, ks, vs, os};
+        return rk::launch_forward(headWidth, false, a, stream);
+    }
+    if (dtype == ROCMKERNELS_DTYPE_FLOAT16) {
+        const rk::HalfForwardArgs a{q, k, v, mask, output, lse, batch, heads, queries, keys, radius, qs, ks, vs, os};
+        return rk::launch_forward_f16(headWidth, a, stream);
+    }
+    return kInvalid;
+}
+
 } // extern "C"

@@ -147,11 +147,13 @@ __device__ __forceinline__ void load_span(float (&r)[N], const float *p, const b
     }
 }
 
-// Stores accumulator tile acc (rows tile_row(v, h) of a 32-feature slice) as 4 groups of 4 contiguous floats.
-template<bool VEC>
+// Stores accumulator tile acc (rows tile_row(v, h) of a 32-feature slice) as 4 groups of 4 contiguous floats; with
+// ROWS = 16 (16-wide heads) only the groups holding features 0..15 (u = 0, 1).
+template<bool VEC, int ROWS = 32>
 __device__ __forceinline__ void store_tile_row(float *p, const f32x16 &acc, const float factor, const int h) {
+    static_assert(ROWS == 16 || ROWS == 32);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < ROWS / 8; ++u) {
         float *dst = p + 8 * u + 4 * h;
         const f32x4 x = {acc[4 * u] * factor, acc[4 * u + 1] * factor, acc[4 * u + 2] * factor, acc[4 * u + 3] * factor};
         if constexpr (VEC) {

@@ -1,4 +1,4 @@
-// FP32 online-softmax attention forward for gfx950 (MI355X), head width 32 or 64.
+// FP32 online-softmax attention forward for gfx950 (MI355X), head width 16, 32 or 64.
 //
 // Replaces the reference's forward kernels: attention_query<false> (Attention.hip:32-115),
 // attention_query_tiled_body (AttentionTile32.h:12-208), attention_query_flash_body (AttentionFlash32.h:23-170),
@@ -30,7 +30,8 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
         const Tensor v, const uint8_t *__restrict__ mask, float *__restrict__ out, const int osb, const int osh, const int ost,
         float *__restrict__ lse, const Shape s, const Plan plan, const float scale) {
     constexpr int HALF = D / 2; // features per lane in row layout
-    constexpr int DT = D / 32;  // 32-feature slices of the output
+    constexpr int DT = (D + 31) / 32; // 32-feature slices of the output (a 16-wide head uses half of one)
+    constexpr int ROWS = D < 32 ? D : 32; // valid features per slice
     constexpr int NREG = STATS ? 0 : 16 * DT;
     constexpr int WG = NI > 0 ? NI * SPLIT : kWaves; // waves per workgroup
 
@@ -97,7 +98,8 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
         t.mask = buffer_load_byte(mbuf, key); // keys >= s.keys read 0: masked
         buffer_load_span<VEC>(t.k, kbuf, key * kstep + 4u * h * HALF);
         if constexpr (!STATS) {
-            const uint32_t vlane = static_cast<uint32_t>(key0 + 4 * h) * vstep + 4u * col;
+            // Lanes past a 16-wide head's last feature read 0 (offset beyond the sequence).
+            const uint32_t vlane = col < ROWS ? static_cast<uint32_t>(key0 + 4 * h) * vstep + 4u * col : kNoRow;
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
 #pragma unroll
@@ -255,10 +257,10 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
 #pragma unroll
         for (int t = 0; t < DT; ++t) {
             if (has_keys) {
-                store_tile_row<VEC>(orow + 32 * t, o[t], factor, h);
+                store_tile_row<VEC, ROWS>(orow + 32 * t, o[t], factor, h);
             } else {
                 const f32x16 fill{};
-                store_tile_row<VEC>(orow + 32 * t, fill + factor, 1.0f, h);
+                store_tile_row<VEC, ROWS>(orow + 32 * t, fill + factor, 1.0f, h);
             }
         }
     }
@@ -286,10 +288,10 @@ void launch(const ForwardArgs &a, const int64_t items, const Plan &plan, hipStre
             a.os.head, a.os.token, a.lse, shape, plan, scale);
 }
 
-// Items (32-query tiles) of 4 waves each that one CU runs at once: 3 at d=32 (about 155 VGPRs per wave), 2 at d=64
+// Items (32-query tiles) of 4 waves each that one CU runs at once: 3 at d<=32 (about 155 VGPRs per wave), 2 at d=64
 // (about 250).
 template<int D>
-constexpr int resident_items_per_cu() { return D == 32 ? 3 : 2; }
+constexpr int resident_items_per_cu() { return D <= 32 ? 3 : 2; }
 
 template<int D, bool STATS, bool VEC>
 void launch_mapped(const ForwardArgs &a, const int64_t items, const int cus, hipStream_t stream) {
@@ -340,7 +342,8 @@ hipError_t launch_forward(const int D, const bool statistics_only, const Forward
     int cus = 0;
     const hipError_t error = compute_units(cus);
     if (error != hipSuccess) return error;
-    if (D == 32) dispatch<32>(statistics_only, a, tiles, cus, stream);
+    if (D == 16) dispatch<16>(statistics_only, a, tiles, cus, stream);
+    else if (D == 32) dispatch<32>(statistics_only, a, tiles, cus, stream);
     else dispatch<64>(statistics_only, a, tiles, cus, stream);
     return hipGetLastError();
 }

@@ -1,0 +1,340 @@
+// FP16-storage online-softmax attention forward for gfx950 (MI355X), head width 16, 32 or 64: the fp16 instance of
+// the reference's attention_generic_forward (Generic/Attention/AttentionGeneric.hip:141-236).
+//
+// The reference reads fp16 Q/K/V, forms scores and the softmax in fp32, rounds each probability to fp16 before the
+// P·V product (accumulated in fp32), and rounds the normalised output to fp16; lse stays fp32. The arithmetic here is
+// the same, on the FP16 matrix cores:
+//
+//   * Sᵀ = K·Qᵀ and Oᵀ += Vᵀ·Pᵀ run on v_mfma_f32_32x32x16_f16 (fp16 operands, fp32 accumulation). A lane of
+//     half-wave h supplies features 16i + 8h .. 16i + 8h + 7 of its key (A) or query (B) row to MFMA i of Sᵀ.
+//   * For Oᵀ the MFMA's 16-long reduction index is mapped onto the Sᵀ accumulator layout: MFMA u takes from lane
+//     (query, h) the probabilities held in accumulator registers 8u .. 8u + 7, i.e. keys tile_row(8u + j, h), so
+//     P is converted to fp16 in place (4 v_cvt_pk_f16_f32) and never leaves the lane; the Vᵀ operand of the same
+//     lane (feature, h) holds V[tile_row(8u + j, h)][feature].
+//   * The online softmax (lazy re-basing, exp2 with the scale folded into one FMA), the masks, the work mapping and
+//     the merge of the waves sharing a query tile follow attention_forward.hip.
+#include "attention_device.hpp"
+#include "attention_launch.hpp"
+
+namespace rk {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Strided fp16 tensor [batch][head][token][D] with contiguous features.
+struct TensorH {
+    const _Float16 *data;
+    int sb, sh, st;
+};
+
+__device__ __forceinline__ f32x16 mfma16(const f16x8 a, const f16x8 b, const f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// Byte extent of one sequence of a strided fp16 tensor: rows 0..rows-1 of `width` halves at `stride` halves.
+__device__ __forceinline__ uint32_t sequence_bytes_h(const int rows, const int stride, const int width) {
+    return static_cast<uint32_t>((static_cast<int64_t>(rows - 1) * stride + width) * 2);
+}
+
+// 8 contiguous halves at byte offset voffset (16-byte aligned when VEC).
+template<bool VEC>
+__device__ __forceinline__ f16x8 load8h(const Buffer b, const uint32_t voffset) {
+    if constexpr (VEC) {
+        return __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(b, static_cast<int>(voffset), 0, 0));
+    } else {
+        f16x8 r;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            r[i] = __builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(b, static_cast<int>(voffset + 2 * i), 0, 0));
+        return r;
+    }
+}
+
+template<int D, bool VEC, int SPLIT>
+__global__ __launch_bounds__(kThreads) void attention_forward_f16_kernel(const TensorH q, const TensorH k, const TensorH v,
+        const uint8_t *__restrict__ mask, _Float16 *__restrict__ out, const int osb, const int osh, const int ost,
+        float *__restrict__ lse, const Shape s, const float scale) {
+    constexpr int KC = D / 16;            // 16-feature chunks of a row: MFMAs per Sᵀ tile
+    constexpr int DT = (D + 31) / 32;     // 32-feature slices of the output
+    constexpr int ROWS = D < 32 ? D : 32; // valid features per slice
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave); // wave-uniform: keeps tile bookkeeping scalar
+    const int col = lane & 31;
+    const int h = lane >> 5;
+
+    const int qtiles = (s.queries + kTile - 1) / kTile;
+    const WorkItem w = work_item<SPLIT>(s, qtiles);
+    const int b = w.b, head = w.head, sub = w.sub;
+    const int qt = s.causal ? qtiles - 1 - w.rank : w.rank;
+    const int q0 = qt * kTile;
+    const int query = q0 + col;
+    const float c2 = scale * kLog2e;
+
+    int first = 0, last = s.keys;
+    if (s.radius >= 0) {
+        first = max(0, q0 - s.radius);
+        last = min(last, q0 + kTile + s.radius);
+    }
+    if (s.causal) last = min(last, q0 + kTile);
+    const int ntiles = (w.valid && last > first) ? (last - first + kTile - 1) / kTile : 0;
+    const int wlo = window_lo(s, query);
+    const int whi = window_hi(s, query);
+
+    auto seq_base = [&](const TensorH &t) {
+        return t.data + (static_cast<int64_t>(b) * t.sb + static_cast<int64_t>(head) * t.sh);
+    };
+    const Buffer qbuf = make_buffer(seq_base(q), sequence_bytes_h(s.queries, q.st, D));
+    const Buffer kbuf = make_buffer(seq_base(k), sequence_bytes_h(s.keys, k.st, D));
+    const Buffer vbuf = make_buffer(seq_base(v), sequence_bytes_h(s.keys, v.st, D));
+    const Buffer mbuf = make_buffer(mask + static_cast<int64_t>(b) * s.keys, static_cast<uint32_t>(s.keys));
+    const uint32_t kstep = 2u * k.st; // bytes between consecutive keys
+    const uint32_t vstep = 2u * v.st;
+
+    f16x8 qr[KC];
+#pragma unroll
+    for (int i = 0; i < KC; ++i) qr[i] = load8h<VEC>(qbuf, static_cast<uint32_t>(query) * (2u * q.st) + 2u * (16 * i + 8 * h));
+
+    constexpr float kLazy = 8.0f; // p = exp2(s·c2 - mc) <= 2^8: also within fp16 range
+    float m_run = -INFINITY;
+    float mc = -INFINITY;
+    float mcx = 0.0f;
+    float l_run = 0.0f;
+    f32x16 o[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t) o[t] = f32x16{};
+
+    struct Tile {
+        f16x8 k[KC];
+        f16x8 v[DT][2];
+        int mask;
+    };
+    auto load_tile = [&](Tile &t, const int key0) __attribute__((always_inline)) {
+        const uint32_t key = static_cast<uint32_t>(key0 + col);
+        t.mask = buffer_load_byte(mbuf, key);
+#pragma unroll
+        for (int i = 0; i < KC; ++i) t.k[i] = load8h<VEC>(kbuf, key * kstep + 2u * (16 * i + 8 * h));
+        // V[key0 + tile_row(8u + j, h)][32 t2 + col]; lanes past a 16-wide head's last feature read 0.
+        const uint32_t vlane = col < ROWS ? static_cast<uint32_t>(key0 + 4 * h) * vstep + 2u * col : kNoRow;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t row = static_cast<uint32_t>(16 * u + 8 * (j >> 2) + (j & 3));
+#pragma unroll
+                for (int t2 = 0; t2 < DT; ++t2)
+                    t.v[t2][u][j] = __builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(vbuf,
+                            static_cast<int>(vlane + 64u * t2), static_cast<int>(row * vstep), 0));
+            }
+        }
+    };
+
+    auto step = [&](Tile &t, const int key0, Tile &next, const int next_key0) __attribute__((always_inline)) {
+        const uint32_t bits = key0 < last ? static_cast<uint32_t>(__ballot(t.mask != 0)) : 0u;
+        if (bits == 0) {
+            load_tile(next, next_key0);
+            return;
+        }
+        f32x16 sc{};
+#pragma unroll
+        for (int i = 0; i < KC; ++i) sc = mfma16(t.k[i], qr[i], sc);
+        __builtin_amdgcn_sched_barrier(0);
+        load_tile(next, next_key0);
+        __builtin_amdgcn_sched_barrier(0);
+
+        if (bits != 0xffffffffu || !tile_in_window(s, q0, key0)) {
+            const uint32_t visible = (bits & bit_range(wlo - key0, whi - key0)) >> (4 * h);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) sc[j] = (visible >> (8 * (j >> 2) + (j & 3))) & 1u ? sc[j] : -INFINITY;
+            if (bits != 0xffffffffu) {
+                // Masked keys contribute exactly nothing, whatever their stored values hold.
+                const uint32_t kept = bits >> (4 * h);
+#pragma unroll
+                for (int u = 0; u < 2; ++u) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const bool ok = (kept >> (16 * u + 8 * (j >> 2) + (j & 3))) & 1u;
+#pragma unroll
+                        for (int t2 = 0; t2 < DT; ++t2) t.v[t2][u][j] = ok ? t.v[t2][u][j] : static_cast<_Float16>(0.0f);
+                    }
+                }
+            }
+        }
+
+        float mx = sc[0];
+#pragma unroll
+        for (int j = 1; j < 16; ++j) mx = fmaxf(mx, sc[j]);
+        mx = halves_max(mx);
+        m_run = fmaxf(m_run, mx);
+
+        auto finish = [&]() __attribute__((always_inline)) {
+            float psum = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                sc[j] = exp2_fast(fmaf(sc[j], c2, -mcx));
+                psum += sc[j];
+            }
+            l_run += psum;
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                f16x8 p;
+#pragma unroll
+                for (int j = 0; j < 8; j += 2) {
+                    const f16x2 pair = {static_cast<_Float16>(sc[8 * u + j]), static_cast<_Float16>(sc[8 * u + j + 1])};
+                    p[j] = pair[0];
+                    p[j + 1] = pair[1];
+                }
+#pragma unroll
+                for (int t2 = 0; t2 < DT; ++t2) o[t2] = mfma16(t.v[t2][u], p, o[t2]);
+            }
+        };
+        if (__ballot(m_run * c2 > mc + kLazy) != 0) {
+            const float mc_new = m_run == -INFINITY ? -INFINITY : m_run * c2;
+            const float alpha = mc_new == -INFINITY ? 1.0f : exp2_fast(mc - mc_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int t2 = 0; t2 < DT; ++t2) o[t2] *= alpha;
+            mc = mc_new;
+            mcx = mc_new == -INFINITY ? 0.0f : mc_new;
+            finish();
+        } else {
+            finish();
+        }
+    };
+
+    const int mine = ntiles > sub ? (ntiles - sub + SPLIT - 1) / SPLIT : 0;
+    Tile ta, tb;
+    if (mine > 0) load_tile(ta, first + sub * kTile);
+    for (int i = 0; i < mine; i += 2) {
+        const int key0 = first + (sub + i * SPLIT) * kTile;
+        step(ta, key0, tb, key0 + SPLIT * kTile);
+        step(tb, key0 + SPLIT * kTile, ta, key0 + 2 * SPLIT * kTile);
+    }
+    const float mc_run = mc;
+
+    float m_all = m_run;
+    float base = 0.0f, l_all = l_run;
+    if constexpr (SPLIT > 1) {
+        constexpr int NREG = 16 * DT;
+        __shared__ float partial[kWaves][NREG + 3][kWave];
+        if (sub > 0) {
+            partial[wave][0][lane] = m_run;
+            partial[wave][1][lane] = l_run;
+            partial[wave][2 + NREG][lane] = mc_run;
+#pragma unroll
+            for (int t = 0; t < DT; ++t) {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) partial[wave][2 + 16 * t + j][lane] = o[t][j];
+            }
+        }
+        __syncthreads();
+        if (sub != 0) return;
+        float mc_all = mc_run;
+#pragma unroll
+        for (int x = 1; x < SPLIT; ++x) {
+            m_all = fmaxf(m_all, partial[wave + x][0][lane]);
+            mc_all = fmaxf(mc_all, partial[wave + x][2 + NREG][lane]);
+        }
+        base = mc_all == -INFINITY ? 0.0f : mc_all;
+        const float a0 = exp2_fast(mc_run - base);
+        l_all = l_run * a0;
+#pragma unroll
+        for (int t = 0; t < DT; ++t) o[t] *= a0;
+#pragma unroll
+        for (int x = 1; x < SPLIT; ++x) {
+            const float aw = exp2_fast(partial[wave + x][2 + NREG][lane] - base);
+            l_all = fmaf(partial[wave + x][1][lane], aw, l_all);
+#pragma unroll
+            for (int t = 0; t < DT; ++t) {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) o[t][j] = fmaf(partial[wave + x][2 + 16 * t + j][lane], aw, o[t][j]);
+            }
+        }
+    } else {
+        base = mc_run == -INFINITY ? 0.0f : mc_run;
+    }
+    l_all = halves_sum(l_all);
+    const float sum_at_max = m_all == -INFINITY ? l_all : l_all * exp2_fast(base - m_all * c2);
+
+    if (!w.valid || query >= s.queries) return;
+    const bool nan_row = isnan(l_all);
+    const bool has_keys = l_all > 0.0f;
+    const float factor = has_keys ? 1.0f / l_all : (nan_row ? NAN : 0.0f);
+    _Float16 *orow = out + static_cast<int64_t>(b) * osb + static_cast<int64_t>(head) * osh + static_cast<int64_t>(query) * ost;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+#pragma unroll
+        for (int u = 0; u < ROWS / 8; ++u) {
+            // Features 32t + 8u + 4h .. +3 of this lane's query: accumulator registers 4u .. 4u + 3.
+            f16x4 x;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[i] = static_cast<_Float16>(has_keys ? o[t][4 * u + i] * factor : factor);
+            _Float16 *dst = orow + 32 * t + 8 * u + 4 * h;
+            if constexpr (VEC) {
+                *reinterpret_cast<f16x4 *>(dst) = x;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) dst[i] = x[i];
+            }
+        }
+    }
+    if (h == 0) {
+        const int64_t row = static_cast<int64_t>(w.seq) * s.queries + query;
+        lse[2 * row] = has_keys ? m_all * scale : (nan_row ? NAN : -INFINITY);
+        lse[2 * row + 1] = has_keys ? sum_at_max : (nan_row ? NAN : 0.0f);
+    }
+}
+
+namespace {
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool aligned8(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
+bool strides8(const rocmkernels_strides &s) { return ((s.batch | s.head | s.token) & 7) == 0; }
+bool strides4(const rocmkernels_strides &s) { return ((s.batch | s.head | s.token) & 3) == 0; }
+
+// Buffer resources use 32-bit byte offsets: every sequence, padded by one 32-row tile, must span less than 2 GiB.
+bool fits_h(const int rows, const rocmkernels_strides &s, const int width) {
+    const long long extent = (static_cast<long long>(rows) + 32) * s.token + width;
+    return s.token >= 0 && extent * 2 < (1ll << 31);
+}
+
+TensorH tensor_h(const void *p, const rocmkernels_strides &s) {
+    return TensorH{static_cast<const _Float16 *>(p), s.batch, s.head, s.token};
+}
+
+template<int D, bool VEC, int SPLIT>
+void launch(const HalfForwardArgs &a, const int64_t items, hipStream_t stream) {
+    const Shape shape{a.batch, a.heads, a.queries, a.keys, a.radius, 0};
+    const float scale = 1.0f / sqrtf(static_cast<float>(D));
+    hipLaunchKernelGGL((attention_forward_f16_kernel<D, VEC, SPLIT>), dim3(workgroups_for(items, SPLIT)), dim3(kThreads), 0, stream,
+            tensor_h(a.q, a.qs), tensor_h(a.k, a.ks), tensor_h(a.v, a.vs), reinterpret_cast<const uint8_t *>(a.mask),
+            static_cast<_Float16 *>(a.output), a.os.batch, a.os.head, a.os.token, a.lse, shape, scale);
+}
+
+template<int D>
+void dispatch(const HalfForwardArgs &a, const int64_t items, hipStream_t stream) {
+    // 128-bit row loads need 16-byte aligned rows; the output's 4-half stores 8-byte alignment.
+    const bool vec = aligned16(a.q) && aligned16(a.k) && strides8(a.qs) && strides8(a.ks) && aligned8(a.output) && strides4(a.os);
+    const int split = forward_split_for(items);
+    if (vec) {
+        if (split == 1) launch<D, true, 1>(a, items, stream);
+        else launch<D, true, 4>(a, items, stream);
+    } else {
+        if (split == 1) launch<D, false, 1>(a, items, stream);
+        else launch<D, false, 4>(a, items, stream);
+    }
+}
+
+} // namespace
+
+hipError_t launch_forward_f16(const int D, const HalfForwardArgs &a, hipStream_t stream) {
+    const int64_t items = static_cast<int64_t>((a.queries + kTile - 1) / kTile) * a.batch * a.heads;
+    if (items > 0x7fffffff || !fits_h(a.queries, a.qs, D) || !fits_h(a.keys, a.ks, D) || !fits_h(a.keys, a.vs, D)) return hipErrorInvalidValue;
+    if (D == 16) dispatch<16>(a, items, stream);
+    else if (D == 32) dispatch<32>(a, items, stream);
+    else dispatch<64>(a, items, stream);
+    return hipGetLastError();
+}
+
+} // namespace rk

@@ -16,6 +16,16 @@ struct ForwardArgs {
     rocmkernels_strides qs, ks, vs, os;
 };
 
+// fp16 storage (attention_generic_forward with dtype Float16): Q/K/V/output hold _Float16, lse stays fp32.
+struct HalfForwardArgs {
+    const void *q, *k, *v;
+    const bool *mask;
+    void *output;
+    float *lse;
+    int batch, heads, queries, keys, radius;
+    rocmkernels_strides qs, ks, vs, os;
+};
+
 struct BackwardArgs {
     const float *q, *k, *v;
     const bool *mask;
@@ -54,8 +64,11 @@ inline unsigned workgroups_for(const long long items, const int split) {
     return static_cast<unsigned>((items + per_group - 1) / per_group);
 }
 
-// Forward pass for head width D (32 or 64). statistics_only writes lse and skips V and the output.
+// Forward pass for head width D (16, 32 or 64). statistics_only writes lse and skips V and the output.
 hipError_t launch_forward(int D, bool statistics_only, const ForwardArgs &a, hipStream_t stream);
+
+// fp16-storage forward for head width D (16, 32 or 64) on the FP16 matrix cores.
+hipError_t launch_forward_f16(int D, const HalfForwardArgs &a, hipStream_t stream);
 
 enum BackwardStage {
     kBackwardAll = 0,    // delta, then dQ, then dK/dV

@@ -3,6 +3,7 @@
 // (ROCmKernels.Common/include/ROCmKernels/Common/Error.hpp:24-45). Prints one line per case; exit code = failures.
 #include <ROCmKernels/Kernels/Attention/Attention.hpp>
 #include <ROCmKernels/Kernels/Attention/Attention64.hpp>
+#include <ROCmKernels/Kernels/Generic/AttentionGeneric.hpp>
 
 #include <cstdio>
 #include <functional>
@@ -61,6 +62,12 @@ int main() {
             [&] { Attention64ForwardEx(dummy, dummy, dummy, mask, dummy, dummy, 1, 1, 1, 1, -3, 1, s, s, s, s); });
     expect_invalid("Attention64BackwardEx flags -1", [&] {
         Attention64BackwardEx(dummy, dummy, dummy, mask, dummy, dummy, dummy, dummy, dummy, dummy, dummy, 1, 1, 1, 1, -1, -1, s, s, s, s, s);
+    });
+    expect_invalid("AttentionGenericForward head width 48", [&] {
+        AttentionGenericForward(dummy, dummy, dummy, mask, dummy, dummy, 1, 1, 1, 1, 48, -1, s, s, s, s, DType::Float32);
+    });
+    expect_invalid("AttentionGenericForward fp16 null output", [&] {
+        AttentionGenericForward(dummy, dummy, dummy, mask, nullptr, dummy, 1, 1, 1, 1, 16, -1, s, s, s, s, DType::Float16);
     });
     std::printf("%d failure(s)\n", failures);
     return failures;

@@ -12,6 +12,11 @@ independently of our oracle:
   autograd for dQ/dK/dV -- an implementation that shares no code with oracle/attention_oracle.c.
 
 Two extra cases exercise the causal extension (no reference counterpart) with the same inputs.
+
+The generic cases follow ROCmKernels.Tests/Generic/AttentionGenericTests.cpp:105-188: head widths 16, 32 and 64,
+shapes (1, 2, 40, 48, radius -1) and (2, 1, 33, 37, radius 3), mask[3] = 0, Q/K/V from seeds 101-103 narrowed to
+the storage type (fp16: round to nearest even, as __float2half_rn does) and the expected forward computed in
+float64 on the narrowed values, as the reference's ComputeReference does (:44-101). Index: generic_cases.json.
 """
 import json
 import os
@@ -34,6 +39,12 @@ CASES = [
     ("ref_d64_b1h2_q4k6", 64, 1, 2, 4, 6, -1, False),        # "64-wide heads"
     ("causal_d32_b1h2_q40k40", 32, 1, 2, 40, 40, -1, True),
     ("causal_d64_b1h2_q64k64_r5", 64, 1, 2, 64, 64, 5, True),
+]
+
+
+GENERIC_CASES = [
+    # width, dtype, batch, heads, queries, keys, radius   (AttentionGenericTests.cpp:153-188)
+    (w, dt, *shape) for w in (16, 32, 64) for dt in ("f32", "f16") for shape in ((1, 2, 40, 48, -1), (2, 1, 33, 37, 3))
 ]
 
 
@@ -78,7 +89,25 @@ def torch_attention(q, k, v, upstream, mask, radius, causal):
     }
 
 
+def generic_case(width, dtype, batch, heads, queries, keys, radius):
+    q, k, v, _, mask = reference_inputs(width, batch, heads, queries, keys)
+    if dtype == "f16":
+        q, k, v = (a.astype(np.float16) for a in (q, k, v))
+    wide = [a.astype(np.float32) for a in (q, k, v)]
+    expected = torch_attention(*wide, np.zeros_like(wide[0]), mask, radius, False)
+    return dict(q=q, k=k, v=v, mask=mask, output=expected["output"], lse=expected["lse"])
+
+
 def main():
+    generic = {}
+    for width, dtype, batch, heads, queries, keys, radius in GENERIC_CASES:
+        name = f"generic_d{width}_{dtype}_b{batch}h{heads}_q{queries}k{keys}" + (f"_r{radius}" if radius >= 0 else "")
+        np.savez_compressed(os.path.join(HERE, f"{name}.npz"), **generic_case(width, dtype, batch, heads, queries, keys, radius))
+        generic[name] = dict(width=width, dtype=dtype, batch=batch, heads=heads, queries=queries, keys=keys, radius=radius)
+        print(name, "written")
+    with open(os.path.join(HERE, "generic_cases.json"), "w") as handle:
+        json.dump(generic, handle, indent=1, sort_keys=True)
+        handle.write("\n")
     index = {}
     for name, width, batch, heads, queries, keys, radius, causal in CASES:
         q, k, v, upstream, mask = reference_inputs(width, batch, heads, queries, keys)

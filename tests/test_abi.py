@@ -92,6 +92,11 @@ BWD_OK = lambda: [_buf()] * 11  # noqa: E731
     ("attention64_fp32_forward_ex", FWD_OK() + [1, 1, 1, 1, -1, 2, S0, S0, S0, S0, None]),
     ("attention64_fp32_forward_ex", FWD_OK()[:3] + [None] + FWD_OK()[4:] + [1, 1, 1, 1, -1, 1, S0, S0, S0, S0, None]),
     ("attention64_fp32_backward_ex", BWD_OK() + [1, 1, 1, 1, -1, -1, S0, S0, S0, S0, S0, None]),
+    ("attention_generic_forward", FWD_OK() + [1, 1, 1, 1, 48, -1, S0, S0, S0, S0, 0, None]),   # head width 48
+    ("attention_generic_forward", FWD_OK() + [1, 1, 1, 1, 16, -2, S0, S0, S0, S0, 1, None]),   # radius < -1
+    ("attention_generic_forward", FWD_OK() + [1, 1, 1, 1, 32, -1, S0, S0, S0, S0, 2, None]),   # unknown dtype
+    ("attention_generic_forward", FWD_OK()[:5] + [None] + [1, 1, 1, 1, 64, -1, S0, S0, S0, S0, 0, None]),
+    ("attention_generic_forward", FWD_OK() + [1, 1, 0, 1, 16, -1, S0, S0, S0, S0, 1, None]),
 ])
 def test_invalid_arguments_return_invalid_value(name, args):
     assert attention.call(name, *args) == attention.HIP_ERROR_INVALID_VALUE

@@ -1,0 +1,131 @@
+"""GPU parity of attention_generic_forward (16-, 32- and 64-wide heads, fp32 or fp16 storage) through the C ABI.
+
+The reference checks this entry point against a double-precision forward on the values the device reads
+(ROCmKernels.Tests/Generic/AttentionGenericTests.cpp:44-146) with max-abs 5e-4 (fp32) and 2e-3 (fp16). Here:
+  fp32: O max-abs <= 1e-5 (the BASELINE tolerance), lse as in test_attention_gpu.py;
+  fp16: O max-abs <= 2e-3 (the reference's, covering the fp16 rounding of P and of O), lse max max-abs <= 1e-5 and
+        lse sum relative <= 1e-5 (scores and sums stay fp32 on fp16 inputs).
+Expected values: golden fixtures at the reference's cases (tests/golden/generic_*.npz) and the CPU oracle run on the
+fp16 inputs widened to float.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from rocmkernels_amd import attention, inputs
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+with open(os.path.join(GOLDEN, "generic_cases.json")) as _handle:
+    GENERIC_CASES = json.load(_handle)
+
+TOL = {"f32": 1e-5, "f16": 2e-3}
+LSE_TOL = 1e-5
+DTYPES = {"f32": (np.float32, torch.float32), "f16": (np.float16, torch.float16)}
+
+
+def check(output, lse, want, dtype, label):
+    output = np.asarray(output, dtype=np.float64)
+    err = np.abs(output - want["output"]).max()
+    assert err <= TOL[dtype], f"{label} O max-abs {err:.3e}"
+    finite = np.isfinite(want["lse"][..., 0])
+    assert np.array_equal(np.isfinite(lse[..., 0]), finite), f"{label} lse finiteness"
+    err_m = np.abs(lse[..., 0][finite] - want["lse"][..., 0][finite]).max(initial=0.0)
+    assert err_m <= LSE_TOL, f"{label} lse max max-abs {err_m:.3e}"
+    assert np.all(lse[..., 1][~finite] == 0.0)
+    scale = max(float(np.abs(want["lse"][..., 1]).max()), 1e-30)
+    err_s = float(np.abs(lse[..., 1] - want["lse"][..., 1]).max()) / scale
+    assert err_s <= LSE_TOL, f"{label} lse sum rel {err_s:.3e}"
+
+
+def run(device, q, k, v, mask, radius=-1, output=None):
+    tq, tk, tv = (torch.from_numpy(np.ascontiguousarray(a)).to(device) for a in (q, k, v))
+    tm = torch.from_numpy(np.ascontiguousarray(mask)).to(device)
+    out, lse = attention.generic_forward(tq, tk, tv, tm, radius=radius, output=output)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy(), lse.cpu().numpy()
+
+
+@pytest.mark.parametrize("name", sorted(GENERIC_CASES))
+def test_generic_reference_cases(device, name):
+    case = GENERIC_CASES[name]
+    data = np.load(os.path.join(GOLDEN, f"{name}.npz"))
+    out, lse = run(device, data["q"], data["k"], data["v"], data["mask"], radius=case["radius"])
+    check(out, lse, {"output": data["output"], "lse": data["lse"]}, case["dtype"], name + " vs golden")
+    wide = [data[key].astype(np.float32) for key in ("q", "k", "v")]
+    want = oracle.attention(*wide, data["mask"], radius=case["radius"])
+    check(out, lse, want, case["dtype"], name + " vs oracle")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+@pytest.mark.parametrize("width", [16, 32, 64])
+@pytest.mark.parametrize("batch,heads,queries,keys,radius,pad", [
+    (2, 3, 100, 70, -1, True),
+    (1, 2, 257, 300, 9, False),
+    (3, 1, 1, 45, -1, True),
+    (1, 1, 64, 64, 0, False),
+    (2, 2, 33, 1, -1, False),
+])
+def test_generic_matches_oracle(device, dtype, width, batch, heads, queries, keys, radius, pad):
+    np_type, _ = DTYPES[dtype]
+    seed = 900 + width + queries
+    q = inputs.normal(seed, (batch, heads, queries, width)).astype(np_type)
+    k = inputs.normal(seed + 1, (batch, heads, keys, width)).astype(np_type)
+    v = inputs.normal(seed + 2, (batch, heads, keys, width)).astype(np_type)
+    mask = np.ones((batch, keys), np.uint8)
+    if pad:
+        lengths = inputs.uniform_int(seed + 3, batch, max(1, keys // 2), keys)
+        mask = (np.arange(keys)[None, :] < lengths[:, None]).astype(np.uint8)
+        mask[0, 0] = 0
+    want = oracle.attention(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32), mask, radius=radius)
+    out, lse = run(device, q, k, v, mask, radius=radius)
+    check(out, lse, want, dtype, f"d{width} {dtype}")
+
+
+@pytest.mark.parametrize("width", [32, 64])
+def test_generic_fp32_is_the_flash_forward(device, width):
+    # fp32 storage at 32/64-wide heads runs the same kernel as attention_fp32_forward / attention64_fp32_forward.
+    q, k, v = (inputs.normal(seed, (2, 2, 150, width)) for seed in (11, 12, 13))
+    mask = np.ones((2, 150), np.uint8)
+    mask[1, 140:] = 0
+    tq, tk, tv, tm = (torch.from_numpy(a).to(device) for a in (q, k, v, mask))
+    a_out, a_lse = attention.generic_forward(tq, tk, tv, tm, radius=20)
+    b_out, b_lse = attention.forward(tq, tk, tv, tm, radius=20, entry="simple")
+    torch.cuda.synchronize()
+    assert torch.equal(a_out.view(torch.int32), b_out.view(torch.int32))
+    assert torch.equal(a_lse.view(torch.int32), b_lse.view(torch.int32))
+
+
+@pytest.mark.parametrize("width", [16, 32, 64])
+def test_generic_fp16_strided_and_unaligned(device, width):
+    # Rows of 2*width halves with an odd element offset: neither 16-byte aligned nor a stride multiple of 8, so the
+    # kernel takes its 16-bit load path; the output is a strided view too.
+    batch, heads, queries, keys = 2, 2, 70, 90
+    base = [inputs.normal(40 + i, (batch, heads, n, 2 * width + 1)).astype(np.float16) for i, n in enumerate((queries, keys, keys))]
+    views = [torch.from_numpy(a).to(device)[..., 1:width + 1] for a in base]
+    mask = np.ones((batch, keys), np.uint8)
+    mask[0, 50:] = 0
+    tm = torch.from_numpy(mask).to(device)
+    out_store = torch.zeros(batch, heads, queries, 3 * width, dtype=torch.float16, device=device)
+    out_view = out_store[..., width:2 * width]
+    out, lse = attention.generic_forward(*views, tm, radius=-1, output=out_view)
+    torch.cuda.synchronize()
+    want = oracle.attention(*(v.float().cpu().numpy() for v in views), mask)
+    check(out.float().cpu().numpy(), lse.cpu().numpy(), want, "f16", f"d{width} strided")
+    assert torch.count_nonzero(out_store[..., :width]) == 0 and torch.count_nonzero(out_store[..., 2 * width:]) == 0
+
+
+def test_generic_fully_masked_batch(device):
+    q, k, v = (inputs.normal(seed, (2, 1, 40, 16)).astype(np.float16) for seed in (1, 2, 3))
+    mask = np.ones((2, 40), np.uint8)
+    mask[1] = 0
+    out, lse = run(device, q, k, v, mask)
+    assert np.all(out[1] == 0.0)
+    assert np.all(lse[1, ..., 0] == -np.inf) and np.all(lse[1, ..., 1] == 0.0)
+    want = oracle.attention(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32), mask)
+    check(out, lse, want, "f16", "masked batch")

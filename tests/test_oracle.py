@@ -101,6 +101,25 @@ def test_oracle_matches_torch_golden(name):
     assert_matches(got, {key: data[key] for key in ("output", "lse", "gq", "gk", "gv")})
 
 
+with open(os.path.join(GOLDEN, "generic_cases.json")) as handle:
+    GENERIC_CASES = json.load(handle)
+
+
+@pytest.mark.parametrize("name", sorted(GENERIC_CASES))
+def test_oracle_matches_generic_golden(name):
+    # The generic forward's reference (AttentionGenericTests.cpp:44-101) is the same double-precision forward as
+    # ReferenceAttention, applied to the values the device reads (fp16 inputs widened to float).
+    case = GENERIC_CASES[name]
+    data = np.load(os.path.join(GOLDEN, f"{name}.npz"))
+    wide = [data[key].astype(np.float32) for key in ("q", "k", "v")]
+    got = oracle.attention(*wide, data["mask"], radius=case["radius"])
+    assert np.abs(got["output"] - data["output"]).max() <= 1e-6
+    finite = np.isfinite(data["lse"][..., 0])
+    assert np.array_equal(np.isfinite(got["lse"][..., 0]), finite)
+    assert np.abs(got["lse"][..., 0][finite] - data["lse"][..., 0][finite]).max() <= 1e-6
+    assert np.abs(got["lse"][..., 1] - data["lse"][..., 1]).max() <= 1e-6 * np.abs(data["lse"][..., 1]).max()
+
+
 @pytest.mark.parametrize("width,batch,heads,queries,keys,radius,causal,padding", [
     (32, 2, 3, 37, 53, -1, False, True),
     (32, 1, 2, 64, 64, 7, False, False),
