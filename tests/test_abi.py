@@ -134,3 +134,13 @@ def test_persistent_work_partition_deals_every_item_once_and_balances(tmp_path):
     result = subprocess.run([binary], capture_output=True, text=True, timeout=60)
     assert result.returncode == 0, result.stdout + result.stderr
     assert "0 failure(s)" in result.stdout
+
+
+def test_autograd_binding_rejects_host_tensors():
+    import torch
+
+    from rocmkernels_amd import autograd
+
+    q = torch.zeros(1, 1, 4, 32)
+    with pytest.raises(ValueError):
+        autograd.attention_fp32(q, q, q, mask=torch.ones(1, 4, dtype=torch.uint8))
