@@ -28,10 +28,12 @@ namespace rk {
 
 enum DqMode { kDqAndDelta = 0, kDeltaOnly = 1, kDqFromDelta = 2, kDeltaZeroDq = 3 };
 
-template<int D, int MODE, bool VEC, int SPLIT>
-__global__ __launch_bounds__(kThreads) void attention_dq_kernel(const Tensor q, const Tensor k, const Tensor v,
-        const uint8_t *__restrict__ mask, const Tensor o, const float *__restrict__ lse, const Tensor du,
-        float *__restrict__ dq, float *__restrict__ delta, const Shape s, const float scale) {
+// NI = 0: items in dispatch order (work_item); NI > 0: persistent grid of NI * SPLIT-wave workgroups taking the NI
+// items of their bin of `plan` (planned_item), as in the forward.
+template<int D, int MODE, bool VEC, int SPLIT, int NI>
+__global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attention_dq_kernel(const Tensor q, const Tensor k,
+        const Tensor v, const uint8_t *__restrict__ mask, const Tensor o, const float *__restrict__ lse, const Tensor du,
+        float *__restrict__ dq, float *__restrict__ delta, const Shape s, const Plan plan, const float scale) {
     constexpr int HALF = D / 2;
     constexpr int DT = D / 32;
 
@@ -40,7 +42,7 @@ __global__ __launch_bounds__(kThreads) void attention_dq_kernel(const Tensor q, 
     const int h = lane >> 5;
 
     const int qtiles = (s.queries + kTile - 1) / kTile;
-    const WorkItem w = work_item<SPLIT>(s, qtiles);
+    const WorkItem w = NI > 0 ? planned_item<SPLIT>(s, plan) : work_item<SPLIT>(s, qtiles);
     const int qt = s.causal ? qtiles - 1 - w.rank : w.rank;
     const int q0 = qt * kTile;
     const int query = q0 + col;
@@ -184,7 +186,7 @@ __global__ __launch_bounds__(kThreads) void attention_dq_kernel(const Tensor q, 
         step(kb, vb, mb, key0 + SPLIT * kTile, ka, va, ma, key0 + 2 * SPLIT * kTile);
     }
 
-    split_sum<SPLIT>(acc, w.sub);
+    split_sum<SPLIT, DT, (NI > 0 ? NI * SPLIT : kWaves)>(acc, w.sub);
     if (w.sub != 0 || !qvalid) return;
     float *dst = dq + row * D;
 #pragma unroll
@@ -411,14 +413,36 @@ bool strides4(const rocmkernels_strides &s) { return ((s.batch | s.head | s.toke
 Tensor tensor(const float *p, const rocmkernels_strides &s) { return Tensor{p, s.batch, s.head, s.token}; }
 
 
-template<int D, int MODE, bool VEC, int SPLIT>
-void launch_dq(const BackwardArgs &a, hipStream_t stream) {
+template<int D, int MODE, bool VEC, int SPLIT, int NI = 0>
+void launch_dq(const BackwardArgs &a, hipStream_t stream, const Plan &plan = Plan{1, 1, 1, 1, 1, 0}) {
     const Shape shape{a.batch, a.heads, a.queries, a.keys, a.radius, a.causal};
     const float scale = 1.0f / sqrtf(static_cast<float>(D));
     const int64_t items = static_cast<int64_t>((a.queries + kTile - 1) / kTile) * a.batch * a.heads;
-    hipLaunchKernelGGL((attention_dq_kernel<D, MODE, VEC, SPLIT>), dim3(workgroups_for(items, SPLIT)), dim3(kThreads), 0, stream,
-            tensor(a.q, a.qs), tensor(a.k, a.ks), tensor(a.v, a.vs), reinterpret_cast<const uint8_t *>(a.mask), tensor(a.output, a.os),
-            a.lse, tensor(a.upstream, a.us), a.gradient_q, a.delta, shape, scale);
+    const unsigned grid = NI > 0 ? static_cast<unsigned>(plan.groups * plan.bins) : workgroups_for(items, SPLIT);
+    const unsigned threads = kWave * (NI > 0 ? NI * SPLIT : kWaves);
+    hipLaunchKernelGGL((attention_dq_kernel<D, MODE, VEC, SPLIT, NI>), dim3(grid), dim3(threads), 0, stream, tensor(a.q, a.qs),
+            tensor(a.k, a.ks), tensor(a.v, a.vs), reinterpret_cast<const uint8_t *>(a.mask), tensor(a.output, a.os), a.lse,
+            tensor(a.upstream, a.us), a.gradient_q, a.delta, shape, plan, scale);
+}
+
+// dQ pass (MODE kDqAndDelta or kDqFromDelta). At d=32 (about 155 VGPRs, 3 waves per SIMD) with more items than CUs but no
+// more than 3 per CU, a persistent cost-balanced grid as in the forward; otherwise SPLIT waves per item in dispatch order.
+template<int D, int MODE, bool VEC>
+void launch_dq_mapped(const BackwardArgs &a, const int cus, hipStream_t stream) {
+    const int qtiles = (a.queries + kTile - 1) / kTile;
+    const int64_t items = static_cast<int64_t>(qtiles) * a.batch * a.heads;
+    if constexpr (D == 32) {
+        if (items > cus && items <= 3ll * cus) {
+            const Plan plan = make_plan(static_cast<int64_t>(a.batch) * a.heads, qtiles, cus, a.causal != 0);
+            if (plan.rounds == 3) launch_dq<D, MODE, VEC, 4, 3>(a, stream, plan);
+            else launch_dq<D, MODE, VEC, 4, 2>(a, stream, plan);
+            return;
+        }
+    }
+    const int split = backward_split_for(items);
+    if (split == 1) launch_dq<D, MODE, VEC, 1>(a, stream);
+    else if (split == 2) launch_dq<D, MODE, VEC, 2>(a, stream);
+    else launch_dq<D, MODE, VEC, 4>(a, stream);
 }
 
 template<int D, bool VEC, int SPLIT, bool FUSED>
@@ -440,8 +464,7 @@ void launch_dkdv_split(const BackwardArgs &a, const int split, hipStream_t strea
 
 
 template<int D, bool VEC>
-hipError_t run(const BackwardStage stage, const BackwardArgs &a, hipStream_t stream) {
-    const int64_t qitems = static_cast<int64_t>((a.queries + kTile - 1) / kTile) * a.batch * a.heads;
+hipError_t run(const BackwardStage stage, const BackwardArgs &a, const int cus, hipStream_t stream) {
     const int64_t kitems = static_cast<int64_t>((a.keys + kTile - 1) / kTile) * a.batch * a.heads;
     if (stage == kBackwardFused) {
         launch_dq<D, kDeltaZeroDq, VEC, 1>(a, stream);
@@ -451,17 +474,9 @@ hipError_t run(const BackwardStage stage, const BackwardArgs &a, hipStream_t str
         return hipGetLastError();
     }
     if (stage == kBackwardAll || stage == kBackwardDelta || stage == kBackwardQuery) {
-        const int split = backward_split_for(qitems);
         if (stage == kBackwardDelta) launch_dq<D, kDeltaOnly, VEC, 1>(a, stream);
-        else if (stage == kBackwardAll) {
-            if (split == 1) launch_dq<D, kDqAndDelta, VEC, 1>(a, stream);
-            else if (split == 2) launch_dq<D, kDqAndDelta, VEC, 2>(a, stream);
-            else launch_dq<D, kDqAndDelta, VEC, 4>(a, stream);
-        } else {
-            if (split == 1) launch_dq<D, kDqFromDelta, VEC, 1>(a, stream);
-            else if (split == 2) launch_dq<D, kDqFromDelta, VEC, 2>(a, stream);
-            else launch_dq<D, kDqFromDelta, VEC, 4>(a, stream);
-        }
+        else if (stage == kBackwardAll) launch_dq_mapped<D, kDqAndDelta, VEC>(a, cus, stream);
+        else launch_dq_mapped<D, kDqFromDelta, VEC>(a, cus, stream);
         const hipError_t error = hipGetLastError();
         if (error != hipSuccess || stage != kBackwardAll) return error;
     }
@@ -481,8 +496,11 @@ hipError_t launch_backward(const int D, const BackwardStage stage, const Backwar
     const bool vec = aligned16(a.q) && aligned16(a.k) && aligned16(a.v) && aligned16(a.output) && aligned16(a.upstream) &&
             aligned16(a.gradient_q) && aligned16(a.gradient_k) && aligned16(a.gradient_v) && strides4(a.qs) && strides4(a.ks) &&
             strides4(a.vs) && strides4(a.os) && strides4(a.us);
-    if (D == 32) return vec ? run<32, true>(stage, a, stream) : run<32, false>(stage, a, stream);
-    return vec ? run<64, true>(stage, a, stream) : run<64, false>(stage, a, stream);
+    int cus = 0;
+    const hipError_t error = compute_units(cus);
+    if (error != hipSuccess) return error;
+    if (D == 32) return vec ? run<32, true>(stage, a, cus, stream) : run<32, false>(stage, a, cus, stream);
+    return vec ? run<64, true>(stage, a, cus, stream) : run<64, false>(stage, a, cus, stream);
 }
 
 } // namespace rk

@@ -241,11 +241,11 @@ __device__ __forceinline__ WorkItem planned_item(const Shape &s, const Plan &pla
 }
 
 // Sums accumulator tiles over the SPLIT waves of an item through LDS; the wave with sub == 0 ends with the total.
-// Every wave of the workgroup must call it (it contains a workgroup barrier when SPLIT > 1).
-template<int SPLIT, int N>
+// Every wave of the WG-wave workgroup must call it (it contains a workgroup barrier when SPLIT > 1).
+template<int SPLIT, int N, int WG = kWaves>
 __device__ __forceinline__ void split_sum(f32x16 (&acc)[N], const int sub) {
     if constexpr (SPLIT > 1) {
-        __shared__ float partial[kWaves][16 * N][kWave];
+        __shared__ float partial[WG][16 * N][kWave];
         const int lane = threadIdx.x & (kWave - 1);
         const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave); // wave-uniform: keeps tile bookkeeping scalar
         __syncthreads(); // a previous call with the same N may still be reading `partial`
