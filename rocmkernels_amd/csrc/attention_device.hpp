@@ -176,6 +176,25 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Keys [first, last) cover every key the 32 queries of query tile qt can see through the causal and radius windows;
+// returns the number of 32-key tiles they span (the work of one forward or dQ item).
+__host__ __device__ inline int forward_key_range(const Shape &s, const int qt, int &first, int &last) {
+    const int q0 = qt * kTile;
+    first = 0;
+    last = s.keys;
+    if (s.radius >= 0) {
+        first = q0 - s.radius > 0 ? q0 - s.radius : 0;
+        last = q0 + kTile + s.radius < last ? q0 + kTile + s.radius : last;
+    }
+    if (s.causal && q0 + kTile < last) last = q0 + kTile;
+    return last > first ? (last - first + kTile - 1) / kTile : 0;
+}
+
+__host__ __device__ inline int forward_item_tiles(const Shape &s, const int qt) {
+    int first, last;
+    return forward_key_range(s, qt, first, last);
+}
+
 // Keys visible to `query` through the causal and radius windows form one interval [lo, hi].
 __device__ __forceinline__ int window_lo(const Shape &s, const int query) { return s.radius >= 0 ? query - s.radius : -0x40000000; }
 __device__ __forceinline__ int window_hi(const Shape &s, const int query) {

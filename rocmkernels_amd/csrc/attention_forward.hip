@@ -49,13 +49,8 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
     const int query = q0 + col;
     const float c2 = scale * kLog2e;
 
-    int first = 0, last = s.keys;
-    if (s.radius >= 0) {
-        first = max(0, q0 - s.radius);
-        last = min(last, q0 + kTile + s.radius);
-    }
-    if (s.causal) last = min(last, q0 + kTile);
-    const int ntiles = (w.valid && last > first) ? (last - first + kTile - 1) / kTile : 0;
+    int first, last;
+    const int ntiles = w.valid ? forward_key_range(s, qt, first, last) : 0;
     // This lane's query sees keys [wlo, whi] through the causal/radius window.
     const int wlo = window_lo(s, query);
     const int whi = window_hi(s, query);
