@@ -124,6 +124,33 @@ def time_graph(launch, steps, results, exact=True):
     return min(times)
 
 
+def measure_rotary(cfg, steps, warmup):
+    """rotary_fp32 on the config's Q and K (32-wide heads only), token-major layout as the reference's bench
+    (RotaryBenchmarks.cpp:52-53): HBM-bound, reported against the 8 TB/s HBM peak with
+    the algorithmic bytes (Q, K read; oq, ok written; cos/sin tables read once)."""
+    import torch
+
+    from rocmkernels_amd import attention, inputs
+
+    if cfg["width"] != 32:
+        return None
+    device = torch.device("cuda:0")
+    batch, heads, length = cfg["batch"], cfg["heads"], cfg["length"]
+    q, k = (torch.from_numpy(inputs.normal(seed, (batch, length, heads, 32))).to(device).permute(0, 2, 1, 3) for seed in (201, 202))
+    cos, sin = (torch.from_numpy(inputs.normal(seed, (batch, length, 32))).to(device) for seed in (203, 204))
+    oq = torch.empty((batch, length, heads, 32), device=device)
+    ok = torch.empty_like(oq)
+
+    def launch():
+        attention.rotary(q, k, cos, sin, out_q=oq, out_k=ok)
+
+    launch()
+    ms = time_graph(launch, steps, [oq, ok])
+    nbytes = 4 * 32 * (4 * batch * heads * length + 2 * batch * length)
+    return {"ms_per_launch": round(ms, 6), "bytes_per_launch": nbytes, "gbps": round(nbytes / (ms * 1e-3) / 1e9, 2),
+            "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 8e12, 4), "shape": f"B{batch} H{heads} L{length} d32"}
+
+
 def cpu_baseline(seconds):
     """The CPU oracle (a C port of the reference's CPU reference) timed on this host's cores on config 2."""
     import numpy as np
@@ -289,6 +316,7 @@ def main():
     for part in ("backward", "backward_fused"):
         if part in measured:
             result[part] = rounded(measured[part])
+    result["rotary"] = measure_rotary(cfg, args.steps, args.warmup)
     result["cpu_baseline"] = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 and args.config == 2 else None
     print(json.dumps(result), flush=True)
 

@@ -180,6 +180,16 @@ ROCMKERNELS_EXPORT int attention_generic_forward(const void *q, const void *k, c
         float *lse, int batch, int heads, int queries, int keys, int headWidth, int radius, rocmkernels_strides qs,
         rocmkernels_strides ks, rocmkernels_strides vs, rocmkernels_strides os, rocmkernels_dtype dtype, hipStream_t stream);
 
+/* ---- rotary position embedding (the step that prepares Q and K) ---------------------------------------- */
+
+/* Replaces rotary_fp32 (reference Positional/Rotary.hpp:9-11, Positional/Rotary.hip:44-56): 32-wide heads, q and k
+ * honour qs and ks, cos and sin hold 32 values per (batch, token) and honour the batch and token entries of cs and
+ * ss. Outputs oq and ok are token-major packed [batch][token][head][32]. backward != 0 applies the transposed
+ * rotation. hipErrorInvalidValue for null pointers or non-positive sizes. */
+ROCMKERNELS_EXPORT int rotary_fp32(const float *q, const float *k, const float *cos, const float *sin, float *oq, float *ok, int batch,
+        int heads, int length, int backward, rocmkernels_strides qs, rocmkernels_strides ks, rocmkernels_strides cs,
+        rocmkernels_strides ss, hipStream_t stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

@@ -78,3 +78,26 @@ def attention(q, k, v, mask, upstream=None, radius=-1, causal=False, threads=Non
     if rc != 0:
         raise RuntimeError("oracle_attention failed")
     return out
+
+
+def rotary(x, cos, sin, backward=False):
+    """Reference-order rotary embedding of x [B][H][L][32] with cos/sin [B][L][32], returned token-major [B][L][H][32].
+
+    Restates ReferenceRotary (ROCmKernels.Tests/PositionalTests.cpp:18-51) in float32 numpy: each product is rounded to
+    float32 before the sum, as the C++ expression ``low * cosineLow - high * sineLow`` is evaluated there:
+    forward  out[c] = x[c]cos[c] - x[c+16]sin[c],   out[c+16] = x[c+16]cos[c+16] + x[c]sin[c+16];
+    backward out[c] = x[c]cos[c] + x[c+16]sin[c+16], out[c+16] = x[c+16]cos[c+16] - x[c]sin[c].
+    """
+    x = np.asarray(x, dtype=np.float32).transpose(0, 2, 1, 3)  # [B][L][H][32]
+    cos = np.asarray(cos, dtype=np.float32)[:, :, None, :]
+    sin = np.asarray(sin, dtype=np.float32)[:, :, None, :]
+    low, high = x[..., :16], x[..., 16:]
+    c_lo, c_hi, s_lo, s_hi = cos[..., :16], cos[..., 16:], sin[..., :16], sin[..., 16:]
+    out = np.empty_like(x)
+    if backward:
+        out[..., :16] = (low * c_lo).astype(np.float32) + (high * s_hi).astype(np.float32)
+        out[..., 16:] = (high * c_hi).astype(np.float32) - (low * s_lo).astype(np.float32)
+    else:
+        out[..., :16] = (low * c_lo).astype(np.float32) - (high * s_lo).astype(np.float32)
+        out[..., 16:] = (high * c_hi).astype(np.float32) + (low * s_hi).astype(np.float32)
+    return np.ascontiguousarray(out)

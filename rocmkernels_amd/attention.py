@@ -53,6 +53,7 @@ ENTRY_POINTS = {
     "attention64_fp32_forward_ex": _FORWARD_CODE,
     "attention64_fp32_backward_ex": _BACKWARD_CODE,
     "attention_generic_forward": [P, P, P, P, P, P, I, I, I, I, I, I, S, S, S, S, ctypes.c_ubyte, P],
+    "rotary_fp32": [P, P, P, P, P, P, I, I, I, I, S, S, S, S, P],
 }
 
 _lib = None
@@ -182,6 +183,30 @@ def generic_forward(q, k, v, mask, radius=-1, output=None, lse=None, stream=None
     check("attention_generic_forward", _ptr(q), _ptr(k), _ptr(v), _ptr(mask), _ptr(output), _ptr(lse), batch, heads, queries,
           k.shape[2], width, radius, strides(q), strides(k), strides(v), strides(output), dtype, _stream(stream))
     return output, lse
+
+
+def table_strides(t):
+    """Strides of a [B][L][32] cos/sin table (the head entry is unused)."""
+    if t.dim() != 3 or t.stride(2) != 1:
+        raise ValueError("expected a [batch][token][32] table with contiguous columns")
+    return Strides(t.stride(0), 0, t.stride(1))
+
+
+def rotary(q, k, cos, sin, backward=False, out_q=None, out_k=None, stream=None):
+    """rotary_fp32 on q/k [B][H][L][32] float32 views and cos/sin [B][L][32] tables; returns (oq, ok) token-major
+    [B][L][H][32]."""
+    torch = _torch()
+    _device_check(q, k, cos, sin)
+    batch, heads, length, width = q.shape
+    if width != 32 or k.shape != q.shape:
+        raise ValueError("rotary_fp32 takes 32-wide q and k of the same shape")
+    if out_q is None:
+        out_q = torch.empty((batch, length, heads, 32), device=q.device, dtype=torch.float32)
+    if out_k is None:
+        out_k = torch.empty((batch, length, heads, 32), device=q.device, dtype=torch.float32)
+    check("rotary_fp32", _ptr(q), _ptr(k), _ptr(cos), _ptr(sin), _ptr(out_q), _ptr(out_k), batch, heads, length,
+          1 if backward else 0, strides(q), strides(k), table_strides(cos), table_strides(sin), _stream(stream))
+    return out_q, out_k
 
 
 def statistics(q, k, mask, radius=-1, lse=None, stream=None):

@@ -223,4 +223,12 @@ int attention_generic_forward(const void *q, const void *k, const void *v, const
     return kInvalid;
 }
 
+// Reference Positional/Rotary.hip:44-56.
+int rotary_fp32(const float *q, const float *k, const float *cos, const float *sin, float *oq, float *ok, int batch, int heads, int length,
+        int backward, rocmkernels_strides qs, rocmkernels_strides ks, rocmkernels_strides cs, rocmkernels_strides ss, hipStream_t stream) {
+    if (!q || !k || !cos || !sin || !oq || !ok || batch <= 0 || heads <= 0 || length <= 0) return kInvalid;
+    const rk::RotaryArgs a{q, k, cos, sin, oq, ok, batch, heads, length, backward != 0, qs, ks, cs, ss};
+    return rk::launch_rotary(a, stream);
+}
+
 } // extern "C"

@@ -67,6 +67,16 @@ inline unsigned workgroups_for(const long long items, const int split) {
 // Forward pass for head width D (16, 32 or 64). statistics_only writes lse and skips V and the output.
 hipError_t launch_forward(int D, bool statistics_only, const ForwardArgs &a, hipStream_t stream);
 
+struct RotaryArgs {
+    const float *q, *k, *cos, *sin;
+    float *oq, *ok;
+    int batch, heads, length, backward;
+    rocmkernels_strides qs, ks, cs, ss;
+};
+
+// 32-wide rotary embedding of Q and K (rotary.hip); outputs token-major [batch][token][head][32].
+hipError_t launch_rotary(const RotaryArgs &a, hipStream_t stream);
+
 // fp16-storage forward for head width D (16, 32 or 64) on the FP16 matrix cores.
 hipError_t launch_forward_f16(int D, const HalfForwardArgs &a, hipStream_t stream);
 

@@ -4,6 +4,7 @@
 #include <ROCmKernels/Kernels/Attention/Attention.hpp>
 #include <ROCmKernels/Kernels/Attention/Attention64.hpp>
 #include <ROCmKernels/Kernels/Generic/AttentionGeneric.hpp>
+#include <ROCmKernels/Kernels/Positional/Rotary.hpp>
 
 #include <cstdio>
 #include <functional>
@@ -69,6 +70,7 @@ int main() {
     expect_invalid("AttentionGenericForward fp16 null output", [&] {
         AttentionGenericForward(dummy, dummy, dummy, mask, nullptr, dummy, 1, 1, 1, 1, 16, -1, s, s, s, s, DType::Float16);
     });
+    expect_invalid("Rotary zero heads", [&] { Rotary(dummy, dummy, dummy, dummy, dummy, dummy, 1, 0, 1, false, s, s, s, s); });
     std::printf("%d failure(s)\n", failures);
     return failures;
 }

@@ -17,6 +17,10 @@ The generic cases follow ROCmKernels.Tests/Generic/AttentionGenericTests.cpp:105
 shapes (1, 2, 40, 48, radius -1) and (2, 1, 33, 37, radius 3), mask[3] = 0, Q/K/V from seeds 101-103 narrowed to
 the storage type (fp16: round to nearest even, as __float2half_rn does) and the expected forward computed in
 float64 on the narrowed values, as the reference's ComputeReference does (:44-101). Index: generic_cases.json.
+
+The rotary cases follow ROCmKernels.Tests/PositionalTests.cpp:53-140: forward (batch 2, heads 3, length 4; Q/K
+seeds 21/22 in [-2, 2), cos/sin seeds 23/24 in [-1, 1)) and backward (1, 2, 3; seeds 31-34), token-major inputs, the
+expected rotation computed in float64 (an evaluation independent of the float32 oracle).
 """
 import json
 import os
@@ -98,7 +102,31 @@ def generic_case(width, dtype, batch, heads, queries, keys, radius):
     return dict(q=q, k=k, v=v, mask=mask, output=expected["output"], lse=expected["lse"])
 
 
+ROTARY_CASES = [  # name, backward, batch, heads, length, seeds (q, k, cos, sin)
+    ("rotary_forward_b2h3l4", False, 2, 3, 4, (21, 22, 23, 24)),
+    ("rotary_backward_b1h2l3", True, 1, 2, 3, (31, 32, 33, 34)),
+]
+
+
+def rotary_float64(x, cos, sin, backward):
+    x, cos, sin = (np.asarray(a, dtype=np.float64) for a in (x, cos, sin))
+    low, high = x[..., :16], x[..., 16:]
+    c_lo, c_hi, s_lo, s_hi = cos[..., :16], cos[..., 16:], sin[..., :16], sin[..., 16:]
+    if backward:
+        return np.concatenate([low * c_lo + high * s_hi, high * c_hi - low * s_lo], axis=-1)
+    return np.concatenate([low * c_lo - high * s_lo, high * c_hi + low * s_hi], axis=-1)
+
+
 def main():
+    for name, backward, batch, heads, length, seeds in ROTARY_CASES:
+        # Token-major [batch][token][head][32] inputs, as the reference's test lays them out; tables [batch][token][32].
+        q, k = (reference_uniform(seed, batch * length * heads * 32, -2.0, 2.0).reshape(batch, length, heads, 32) for seed in seeds[:2])
+        cos, sin = (reference_uniform(seed, batch * length * 32, -1.0, 1.0).reshape(batch, length, 32) for seed in seeds[2:])
+        expected_q = rotary_float64(q, cos[:, :, None, :], sin[:, :, None, :], backward)
+        expected_k = rotary_float64(k, cos[:, :, None, :], sin[:, :, None, :], backward)
+        np.savez_compressed(os.path.join(HERE, f"{name}.npz"), q=q, k=k, cos=cos, sin=sin, backward=np.array(backward),
+                            expected_q=expected_q, expected_k=expected_k)
+        print(name, "written")
     generic = {}
     for width, dtype, batch, heads, queries, keys, radius in GENERIC_CASES:
         name = f"generic_d{width}_{dtype}_b{batch}h{heads}_q{queries}k{keys}" + (f"_r{radius}" if radius >= 0 else "")

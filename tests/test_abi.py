@@ -97,6 +97,9 @@ BWD_OK = lambda: [_buf()] * 11  # noqa: E731
     ("attention_generic_forward", FWD_OK() + [1, 1, 1, 1, 32, -1, S0, S0, S0, S0, 2, None]),   # unknown dtype
     ("attention_generic_forward", FWD_OK()[:5] + [None] + [1, 1, 1, 1, 64, -1, S0, S0, S0, S0, 0, None]),
     ("attention_generic_forward", FWD_OK() + [1, 1, 0, 1, 16, -1, S0, S0, S0, S0, 1, None]),
+    ("rotary_fp32", [None] + FWD_OK()[1:] + [1, 1, 1, 0, S0, S0, S0, S0, None]),
+    ("rotary_fp32", FWD_OK() + [1, 0, 1, 1, S0, S0, S0, S0, None]),
+    ("rotary_fp32", FWD_OK() + [1, 1, -3, 0, S0, S0, S0, S0, None]),
 ])
 def test_invalid_arguments_return_invalid_value(name, args):
     assert attention.call(name, *args) == attention.HIP_ERROR_INVALID_VALUE

@@ -239,3 +239,44 @@ def test_pins_catch_planted_mistakes(mutation, tmp_path):
         except AssertionError:
             failures += 1
     assert failures == len(GOLDEN_CASES)
+
+
+# ---- rotary (ReferenceRotary, PositionalTests.cpp:18-51) ---------------------------------------------------------
+
+@pytest.mark.parametrize("name", ["rotary_forward_b2h3l4", "rotary_backward_b1h2l3"])
+def test_rotary_oracle_matches_float64_golden(name):
+    # The reference's own cases and tolerance (PositionalTests.cpp:53-140, CheckClose 1e-6); inputs token-major.
+    data = np.load(os.path.join(GOLDEN, f"{name}.npz"))
+    backward = bool(data["backward"])
+    for x, expected in ((data["q"], data["expected_q"]), (data["k"], data["expected_k"])):
+        got = oracle.rotary(x.transpose(0, 2, 1, 3), data["cos"], data["sin"], backward=backward)
+        assert got.shape == expected.shape
+        assert np.abs(got - expected).max() <= 1e-6
+
+
+def rope_tables(batch, length, seed):
+    """cos/sin of real rotation angles, the same angle for column c and c + 16 (as rotary embeddings build them)."""
+    angles = inputs.normal(seed, (batch, length, 16)).astype(np.float64) * 3.0
+    cos = np.concatenate([np.cos(angles)] * 2, axis=-1).astype(np.float32)
+    sin = np.concatenate([np.sin(angles)] * 2, axis=-1).astype(np.float32)
+    return cos, sin
+
+
+def test_rotary_closed_forms():
+    x = inputs.normal(5, (2, 3, 7, 32))
+    # Angle 0 is the identity, exactly.
+    ones, zeros = np.ones((2, 7, 32), np.float32), np.zeros((2, 7, 32), np.float32)
+    assert np.array_equal(oracle.rotary(x, ones, zeros), x.transpose(0, 2, 1, 3))
+    assert np.array_equal(oracle.rotary(x, ones, zeros, backward=True), x.transpose(0, 2, 1, 3))
+    # A quarter turn maps (lo, hi) to (-hi, lo), exactly.
+    quarter = oracle.rotary(x, zeros, ones)
+    xt = x.transpose(0, 2, 1, 3)
+    assert np.array_equal(quarter[..., :16], -xt[..., 16:]) and np.array_equal(quarter[..., 16:], xt[..., :16])
+    # Real rotations: pair norms are kept, and the backward undoes the forward.
+    cos, sin = rope_tables(2, 7, 6)
+    rotated = oracle.rotary(x, cos, sin)
+    norm_in = np.hypot(xt[..., :16].astype(np.float64), xt[..., 16:])
+    norm_out = np.hypot(rotated[..., :16].astype(np.float64), rotated[..., 16:])
+    assert np.abs(norm_in - norm_out).max() <= 1e-5
+    back = oracle.rotary(rotated.transpose(0, 2, 1, 3), cos, sin, backward=True)
+    assert np.abs(back - xt).max() <= 1e-5

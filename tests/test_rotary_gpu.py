@@ -1,0 +1,68 @@
+"""GPU parity of rotary_fp32 (32-wide rotary embedding) through the C ABI: bit-identical to the CPU oracle's restatement
+of the reference's ReferenceRotary (PositionalTests.cpp:18-51), which evaluates each product in float32 before the
+sum exactly as the kernel does; the reference's own cases are also checked against float64 within its 1e-6."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from rocmkernels_amd import attention, inputs
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def run(device, q, k, cos, sin, backward, token_major):
+    # token_major: q/k arrays are [B][L][H][32] (the reference's layout), passed as permuted [b][h][t][d] views.
+    tq, tk = (torch.from_numpy(np.ascontiguousarray(a)).to(device) for a in (q, k))
+    if token_major:
+        tq, tk = tq.permute(0, 2, 1, 3), tk.permute(0, 2, 1, 3)
+    tc, ts = (torch.from_numpy(np.ascontiguousarray(a)).to(device) for a in (cos, sin))
+    oq, ok = attention.rotary(tq, tk, tc, ts, backward=backward)
+    torch.cuda.synchronize()
+    return oq.cpu().numpy(), ok.cpu().numpy(), tq.cpu().numpy(), tk.cpu().numpy()
+
+
+@pytest.mark.parametrize("name", ["rotary_forward_b2h3l4", "rotary_backward_b1h2l3"])
+def test_rotary_reference_cases(device, name):
+    data = np.load(os.path.join(GOLDEN, f"{name}.npz"))
+    backward = bool(data["backward"])
+    oq, ok, hq, hk = run(device, data["q"], data["k"], data["cos"], data["sin"], backward, token_major=True)
+    assert np.abs(oq - data["expected_q"]).max() <= 1e-6 and np.abs(ok - data["expected_k"]).max() <= 1e-6
+    assert np.array_equal(oq, oracle.rotary(hq, data["cos"], data["sin"], backward))
+    assert np.array_equal(ok, oracle.rotary(hk, data["cos"], data["sin"], backward))
+
+
+@pytest.mark.parametrize("backward", [False, True])
+@pytest.mark.parametrize("batch,heads,length,token_major", [
+    (2, 12, 1024, True),
+    (3, 5, 77, False),
+    (1, 1, 1, True),
+    (4, 16, 300, False),
+])
+def test_rotary_matches_oracle_bitwise(device, backward, batch, heads, length, token_major):
+    shape = (batch, length, heads, 32) if token_major else (batch, heads, length, 32)
+    q, k = inputs.normal(50 + length, shape), inputs.normal(51 + length, shape)
+    cos, sin = inputs.normal(52, (batch, length, 32)), inputs.normal(53, (batch, length, 32))
+    oq, ok, hq, hk = run(device, q, k, cos, sin, backward, token_major)
+    assert np.array_equal(oq, oracle.rotary(hq, cos, sin, backward))
+    assert np.array_equal(ok, oracle.rotary(hk, cos, sin, backward))
+
+
+def test_rotary_strided_unaligned_and_broadcast_tables(device):
+    # Rows of 33 floats with an odd offset (32-bit path) and tables shared by the batch (batch stride 0).
+    batch, heads, length = 2, 3, 50
+    base = torch.from_numpy(inputs.normal(7, (batch, heads, length, 33 * 2))).to(device)
+    q = base[..., 1:33]
+    k = base[..., 34:66]
+    table = torch.from_numpy(inputs.normal(8, (1, length, 64))).to(device)
+    cos = table[..., :32].expand(batch, length, 32)
+    sin = table[..., 32:].expand(batch, length, 32)
+    oq, ok = attention.rotary(q, k, cos, sin)
+    torch.cuda.synchronize()
+    hq, hk, hc, hs = (t.cpu().numpy() for t in (q, k, cos, sin))
+    assert np.array_equal(oq.cpu().numpy(), oracle.rotary(hq, hc, hs))
+    assert np.array_equal(ok.cpu().numpy(), oracle.rotary(hk, hc, hs))
