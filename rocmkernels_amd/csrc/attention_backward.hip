@@ -29,11 +29,11 @@ namespace rk {
 enum DqMode { kDqAndDelta = 0, kDeltaOnly = 1, kDqFromDelta = 2, kDeltaZeroDq = 3 };
 
 // NI = 0: items in dispatch order (work_item); NI > 0: persistent grid of NI * SPLIT-wave workgroups taking the NI
-// items of their bin of `plan` (planned_item), as in the forward.
+// items of their bin from the launch's item table (planned_item), as in the forward.
 template<int D, int MODE, bool VEC, int SPLIT, int NI>
 __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attention_dq_kernel(const Tensor q, const Tensor k,
         const Tensor v, const uint8_t *__restrict__ mask, const Tensor o, const float *__restrict__ lse, const Tensor du,
-        float *__restrict__ dq, float *__restrict__ delta, const Shape s, const Plan plan, const float scale) {
+        float *__restrict__ dq, float *__restrict__ delta, const Shape s, const ItemTable<NI> items, const float scale) {
     constexpr int HALF = D / 2;
     constexpr int DT = D / 32;
 
@@ -42,7 +42,10 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
     const int h = lane >> 5;
 
     const int qtiles = (s.queries + kTile - 1) / kTile;
-    const WorkItem w = NI > 0 ? planned_item<SPLIT>(s, plan) : work_item<SPLIT>(s, qtiles);
+    const WorkItem w = [&] {
+        if constexpr (NI > 0) return planned_item<SPLIT, NI>(s, items);
+        else return work_item<SPLIT>(s, qtiles);
+    }();
     const int qt = s.causal ? qtiles - 1 - w.rank : w.rank;
     const int q0 = qt * kTile;
     const int query = q0 + col;
@@ -170,13 +173,13 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
         }
     };
 
-    // Tiles sub, sub + SPLIT, ...; the count is rounded up to even so the loop body is two straight-line steps.
-    const int mine = ntiles > w.sub ? (ntiles - w.sub + SPLIT - 1) / SPLIT : 0;
+    // Tiles lead, lead + SPLIT, ...; the count is rounded up to even so the loop body is two straight-line steps.
+    const int mine = ntiles > w.lead ? (ntiles - w.lead + SPLIT - 1) / SPLIT : 0;
     float ka[HALF], va[HALF], kb[HALF], vb[HALF];
     int ma = 0, mb = 0;
-    if (mine > 0) load_rows(ka, va, ma, first + w.sub * kTile);
+    if (mine > 0) load_rows(ka, va, ma, first + w.lead * kTile);
     for (int i = 0; i < mine; i += 2) {
-        const int key0 = first + (w.sub + i * SPLIT) * kTile;
+        const int key0 = first + (w.lead + i * SPLIT) * kTile;
         step(ka, va, ma, key0, kb, vb, mb, key0 + SPLIT * kTile);
         step(kb, vb, mb, key0 + SPLIT * kTile, ka, va, ma, key0 + 2 * SPLIT * kTile);
     }
@@ -379,12 +382,12 @@ __global__ __launch_bounds__(kThreads) void attention_dkdv_kernel(const Tensor q
         }
     };
 
-    // Tiles sub, sub + SPLIT, ...; the count is rounded up to even so the loop body is two straight-line steps.
-    const int mine = ntiles > w.sub ? (ntiles - w.sub + SPLIT - 1) / SPLIT : 0;
+    // Tiles lead, lead + SPLIT, ...; the count is rounded up to even so the loop body is two straight-line steps.
+    const int mine = ntiles > w.lead ? (ntiles - w.lead + SPLIT - 1) / SPLIT : 0;
     Rows ra, rb;
-    if (mine > 0) load_rows(ra, first + w.sub * kTile);
+    if (mine > 0) load_rows(ra, first + w.lead * kTile);
     for (int i = 0; i < mine; i += 2) {
-        const int q0 = first + (w.sub + i * SPLIT) * kTile;
+        const int q0 = first + (w.lead + i * SPLIT) * kTile;
         step(ra, q0, rb, q0 + SPLIT * kTile);
         step(rb, q0 + SPLIT * kTile, ra, q0 + 2 * SPLIT * kTile);
     }
@@ -409,15 +412,15 @@ Tensor tensor(const float *p, const rocmkernels_strides &s) { return Tensor{p, s
 
 
 template<int D, int MODE, bool VEC, int SPLIT, int NI = 0>
-void launch_dq(const BackwardArgs &a, hipStream_t stream, const Plan &plan = Plan{1, 1, 1, 1, 1, 0}) {
+void launch_dq(const BackwardArgs &a, hipStream_t stream, const unsigned planned_grid = 0, const ItemTable<NI> &table = ItemTable<NI>{}) {
     const Shape shape{a.batch, a.heads, a.queries, a.keys, a.radius, a.causal};
     const float scale = 1.0f / sqrtf(static_cast<float>(D));
     const int64_t items = static_cast<int64_t>((a.queries + kTile - 1) / kTile) * a.batch * a.heads;
-    const unsigned grid = NI > 0 ? static_cast<unsigned>(plan.groups * plan.bins) : workgroups_for(items, SPLIT);
+    const unsigned grid = NI > 0 ? planned_grid : workgroups_for(items, SPLIT);
     const unsigned threads = kWave * (NI > 0 ? NI * SPLIT : kWaves);
     hipLaunchKernelGGL((attention_dq_kernel<D, MODE, VEC, SPLIT, NI>), dim3(grid), dim3(threads), 0, stream, tensor(a.q, a.qs),
             tensor(a.k, a.ks), tensor(a.v, a.vs), reinterpret_cast<const uint8_t *>(a.mask), tensor(a.output, a.os), a.lse,
-            tensor(a.upstream, a.us), a.gradient_q, a.delta, shape, plan, scale);
+            tensor(a.upstream, a.us), a.gradient_q, a.delta, shape, table, scale);
 }
 
 // dQ pass (MODE kDqAndDelta or kDqFromDelta). At d=32 (about 155 VGPRs, 3 waves per SIMD) with more items than CUs but no
@@ -428,10 +431,18 @@ void launch_dq_mapped(const BackwardArgs &a, const int cus, hipStream_t stream) 
     const int64_t items = static_cast<int64_t>(qtiles) * a.batch * a.heads;
     if constexpr (D == 32) {
         if (items > cus && items <= 3ll * cus) {
+            const Shape shape{a.batch, a.heads, a.queries, a.keys, a.radius, a.causal};
             const Plan plan = make_plan(static_cast<int64_t>(a.batch) * a.heads, qtiles, cus, a.causal != 0);
-            if (plan.rounds == 3) launch_dq<D, MODE, VEC, 4, 3>(a, stream, plan);
-            else launch_dq<D, MODE, VEC, 4, 2>(a, stream, plan);
-            return;
+            const unsigned grid = static_cast<unsigned>(plan.groups * plan.bins);
+            if (plan.rounds == 3) {
+                if (const ItemTable<3> *table = item_table<3>(shape, plan)) {
+                    launch_dq<D, MODE, VEC, 4, 3>(a, stream, grid, *table);
+                    return;
+                }
+            } else if (const ItemTable<2> *table = item_table<2>(shape, plan)) {
+                launch_dq<D, MODE, VEC, 4, 2>(a, stream, grid, *table);
+                return;
+            }
         }
     }
     const int split = backward_split_for(items);

@@ -176,6 +176,65 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// ---- coalesced row tiles -----------------------------------------------------------------------------------
+// Row-layout operands (a lane holds D/2 contiguous features of one row) read straight from memory need 128-bit
+// loads that each touch 32 different 128-byte lines. When every wave of the chip asks for its first tiles at once,
+// those scattered requests queue up: the last waves of a CU received their first tile 3.4 us after launch against
+// 1.6 us for loads that cover whole lines (12 waves per CU, 12 KiB each). So a 32-row tile is read with loads that
+// cover whole lines (load i, lane L: 16-byte chunk i*64 + L of the tile in row-major order), written to the wave's
+// LDS slot and read back in row layout. Chunk c of row r is stored at chunk position c ^ row_swizzle(r), which keeps
+// the writes and the row-layout reads free of LDS bank conflicts (for 8-lane phases over 32 banks and for 16-lane
+// phases over 64 banks alike).
+template<int D>
+struct RowTile {
+    f32x4 x[D / 8]; // the tile's 32 * D floats, 16 bytes per lane per load
+};
+
+template<int D>
+__device__ __forceinline__ constexpr int row_swizzle(const int r) {
+    if constexpr (D == 64) return r & 15;
+    else if constexpr (D == 32) return (r & 7) ^ ((r >> 3) & 1);
+    else return ((r >> 1) ^ (r >> 2)) & 3;
+}
+
+// Issues the loads of the 32 rows that start at byte offset row0 of b, rows `step` bytes apart (rows at or beyond
+// the buffer's extent read 0: the range check covers voffset + soffset).
+template<int D>
+__device__ __forceinline__ void load_row_tile(RowTile<D> &t, const Buffer b, const uint32_t step, const uint32_t row0) {
+    constexpr int CPR = D / 4;        // chunks per row
+    constexpr int RPL = kWave / CPR;  // rows per load
+    const int lane = threadIdx.x & (kWave - 1);
+    const uint32_t voffset = static_cast<uint32_t>(lane / CPR) * step + 16u * static_cast<uint32_t>(lane % CPR);
+#pragma unroll
+    for (int i = 0; i < D / 8; ++i) t.x[i] = buffer_load4(b, voffset, row0 + static_cast<uint32_t>(i * RPL) * step);
+}
+
+// Passes a loaded tile through the wave's LDS slot (32 * D floats, 16-byte aligned) into row layout: lane
+// (col, h) receives features h*D/2 .. h*D/2 + D/2 - 1 of row col.
+template<int D>
+__device__ __forceinline__ void stage_row_tile(float *slot, const RowTile<D> &t, float (&r)[D / 2]) {
+    constexpr int CPR = D / 4;
+    constexpr int RPL = kWave / CPR;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int col = lane & 31;
+    const int h = lane >> 5;
+    wave_lds_sync(); // the previous tile's row-layout reads come first
+#pragma unroll
+    for (int i = 0; i < D / 8; ++i) {
+        const int row = i * RPL + lane / CPR;
+        *reinterpret_cast<f32x4 *>(slot + row * D + 4 * ((lane % CPR) ^ row_swizzle<D>(row))) = t.x[i];
+    }
+    wave_lds_sync();
+#pragma unroll
+    for (int k = 0; k < CPR / 2; ++k) {
+        const f32x4 x = *reinterpret_cast<const f32x4 *>(slot + col * D + 4 * ((h * (CPR / 2) + k) ^ row_swizzle<D>(col)));
+        r[4 * k + 0] = x[0];
+        r[4 * k + 1] = x[1];
+        r[4 * k + 2] = x[2];
+        r[4 * k + 3] = x[3];
+    }
+}
+
 // Keys [first, last) cover every key the 32 queries of query tile qt can see through the causal and radius windows;
 // returns the number of 32-key tiles they span (the work of one forward or dQ item).
 __host__ __device__ inline int forward_key_range(const Shape &s, const int qt, int &first, int &last) {
@@ -220,6 +279,7 @@ __device__ __forceinline__ int window_query_hi(const Shape &s, const int key) { 
 struct WorkItem {
     int seq, b, head, rank, sub;
     int split; // waves sharing the item
+    int lead;  // index of this wave's first tile among the item's tiles; it then takes every split-th tile
     bool valid;
 };
 
@@ -231,6 +291,7 @@ __device__ __forceinline__ WorkItem work_item(const Shape &s, const int tiles_pe
     WorkItem w;
     w.sub = wave % SPLIT;
     w.split = SPLIT;
+    w.lead = w.sub;
     w.valid = item < seqs * tiles_per_seq;
     w.rank = item / seqs;
     w.seq = item - w.rank * seqs;
@@ -240,23 +301,48 @@ __device__ __forceinline__ WorkItem work_item(const Shape &s, const int tiles_pe
 }
 
 // Planned mapping (persistent grid, see attention_plan.hpp): the NI * SPLIT waves of workgroup blockIdx.x take the NI
-// items of its bin, item i on waves i*SPLIT .. i*SPLIT + SPLIT - 1. Waves are dealt to the 4 SIMDs round-robin, so with
-// SPLIT = 4 every SIMD runs one quarter of every item of the bin and carries a quarter of the bin's cost-balanced load.
-template<int SPLIT>
-__device__ __forceinline__ WorkItem planned_item(const Shape &s, const Plan &plan) {
+// items of its bin from the launch's item table, item i on waves i*SPLIT .. i*SPLIT + SPLIT - 1. Waves are dealt to
+// the 4 SIMDs round-robin (wave w and w + 4 share a SIMD), so with SPLIT = 4 every SIMD runs one quarter of every item
+// of the bin, and the table's rotations deal the items' leftover tiles round-robin over the SIMDs. (Dealing them
+// always from sub 0 put 9% more tiles than the average on one SIMD at 3 items per bin.)
+template<int SPLIT, int NI>
+__device__ __forceinline__ WorkItem planned_item(const Shape &s, const ItemTable<NI> &items) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave); // wave-uniform: keeps tile bookkeeping scalar
-    const int group = static_cast<int>(blockIdx.x) % plan.groups;
-    const int bin = static_cast<int>(blockIdx.x) / plan.groups;
-    const int p = plan_position(plan, bin, wave / SPLIT);
+    const uint32_t e = items.entry[static_cast<int>(blockIdx.x) * NI + wave / SPLIT];
     WorkItem w;
     w.sub = wave % SPLIT;
     w.split = SPLIT;
-    w.valid = p < plan.seqs * plan.tiles;
-    w.rank = w.valid ? p / plan.seqs : 0;
-    w.seq = group + plan.groups * (w.valid ? p - w.rank * plan.seqs : 0);
-    w.b = w.seq / s.heads;
-    w.head = w.seq - w.b * s.heads;
+    w.valid = e != kNoItem;
+    // An empty slot reads sequence 0 (its loads stay in bounds) and visits no tile.
+    w.b = w.valid ? static_cast<int>(e & 1023u) : 0;
+    w.head = w.valid ? static_cast<int>((e >> 10) & 1023u) : 0;
+    w.rank = w.valid ? static_cast<int>((e >> 20) & 1023u) : 0;
+    w.lead = plan_lead(static_cast<int>(e >> 30), w.sub, SPLIT);
+    w.seq = w.b * s.heads + w.head;
     return w;
+}
+
+// Host: the item table of a planned launch over shape s (forward and dQ items: 32-query tiles), or null when the
+// launch does not fit one. Kept per host thread for the last shape, so repeated launches do not rebuild it.
+template<int NI>
+inline const ItemTable<NI> *item_table(const Shape &s, const Plan &p) {
+    struct Cache {
+        Shape s;
+        Plan p;
+        bool ok;
+        ItemTable<NI> table;
+    };
+    thread_local Cache cache{Shape{}, Plan{}, false, {}};
+    const bool same = cache.ok && cache.s.batch == s.batch && cache.s.heads == s.heads && cache.s.queries == s.queries &&
+            cache.s.keys == s.keys && cache.s.radius == s.radius && cache.s.causal == s.causal && cache.p.groups == p.groups &&
+            cache.p.bins == p.bins && cache.p.seqs == p.seqs && cache.p.tiles == p.tiles && cache.p.rounds == p.rounds &&
+            cache.p.reverse == p.reverse;
+    if (!same) {
+        cache.ok = fill_item_table(cache.table.entry, p, NI, s.heads, [&](const int tile) { return forward_item_tiles(s, tile); });
+        cache.s = s;
+        cache.p = p;
+    }
+    return cache.ok ? &cache.table : nullptr;
 }
 
 // Sums accumulator tiles over the SPLIT waves of an item through LDS; the wave with sub == 0 ends with the total.

@@ -17,6 +17,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <stdint.h>
+
 namespace rk {
 
 struct Plan {
@@ -52,6 +54,71 @@ __host__ __device__ inline PlanItem plan_item(const Plan &p, const int x, const 
     const int rank = position / p.seqs;
     const int local = position - rank * p.seqs;
     return PlanItem{x + p.groups * local, p.reverse ? p.tiles - 1 - rank : rank};
+}
+
+// The SPLIT waves of an item take its tiles round-robin, and an item of c tiles leaves c mod split of them over.
+// They are dealt round-robin over the subs across the bin: item i's tile j goes to sub (j + r) mod split, r = the
+// rotation of slot i = the tiles of items 0 .. i-1. Wave `sub` of every slot runs on the same SIMD, so the SIMDs'
+// tile counts then differ by at most one. cost(tile) = tiles streamed by the item of that 32-row tile.
+template<class Cost>
+inline int plan_rotation(const Plan &p, const int lb, const int slot, const Cost &cost) {
+    int rotation = 0;
+    for (int j = 0; j < slot; ++j) {
+        const int position = plan_position(p, lb, j);
+        if (position < p.seqs * p.tiles) rotation += cost(plan_item(p, 0, position).tile);
+    }
+    return rotation;
+}
+
+// Index (among its item's tiles) of the first tile taken by wave `sub` of an item whose slot has this rotation.
+__host__ __device__ inline int plan_lead(const int rotation, const int sub, const int split) {
+    return (sub + split - rotation % split) % split;
+}
+
+// ---- item table -------------------------------------------------------------------------------------------
+// A persistent launch reads its items from a table passed by value in the kernel arguments: one scalar load per
+// wave instead of the plan arithmetic above. The twelve waves of a CU share one scalar unit, and that arithmetic
+// (integer divisions, the rotation loop) delayed the last waves' first loads by about 3 us at the 24 x 1024 causal
+// shape. Entry g * ni + slot: batch in bits 0-9, head in 10-19, rank in 20-29, rotation mod 4 in 30-31.
+constexpr int kMaxTableItems = 768; // 3 items on each of 256 CUs
+constexpr int kItemFieldLimit = 1024;
+constexpr uint32_t kNoItem = 0xffffffffu;
+
+template<int NI>
+struct ItemTable {
+    uint32_t entry[NI > 0 ? kMaxTableItems : 1];
+};
+
+__host__ __device__ inline uint32_t pack_item(const int batch, const int head, const int rank, const int rotation) {
+    return static_cast<uint32_t>(batch) | static_cast<uint32_t>(head) << 10 | static_cast<uint32_t>(rank) << 20 |
+            static_cast<uint32_t>(rotation & 3) << 30;
+}
+
+// Fills entry[0 .. groups * bins * ni) for a plan of sequences with `heads` heads each; false (table untouched
+// beyond what was written) when the launch does not fit the table.
+template<class Cost>
+inline bool fill_item_table(uint32_t *entry, const Plan &p, const int ni, const int heads, const Cost &cost) {
+    const long long grid = static_cast<long long>(p.groups) * p.bins;
+    const long long sequences = static_cast<long long>(p.groups) * p.seqs;
+    if (grid * ni > kMaxTableItems || p.rounds > ni || p.tiles > kItemFieldLimit || heads > kItemFieldLimit ||
+            sequences / heads > kItemFieldLimit)
+        return false;
+    for (int g = 0; g < grid; ++g) {
+        const int x = g % p.groups, lb = g / p.groups;
+        int rotation = 0;
+        for (int slot = 0; slot < ni; ++slot) {
+            const int position = plan_position(p, lb, slot);
+            if (position >= p.seqs * p.tiles) {
+                entry[g * ni + slot] = kNoItem;
+                continue;
+            }
+            const PlanItem it = plan_item(p, x, position);
+            const int rank = p.reverse ? p.tiles - 1 - it.tile : it.tile;
+            entry[g * ni + slot] = pack_item(it.seq / heads, it.seq % heads, rank, rotation);
+            rotation += cost(it.tile);
+        }
+    }
+    return true;
 }
 
 // Plan for `seqs` sequences of `tiles` items each over at most `workgroups` workgroups (the CU count).

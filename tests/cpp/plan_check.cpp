@@ -1,10 +1,13 @@
 // Host-side check of the persistent-grid work partition (rocmkernels_amd/csrc/attention_plan.hpp): every item of
 // every sequence is dealt to exactly one (workgroup, round) slot, and for causal item costs (tile t streams t + 1 key
 // tiles) the busiest workgroup carries no more than the average plus one item (any whole-item partition can do no
-// better when the last round is partial) and, when every round is full, at most a few percent more than the average.
+// better when the last round is partial) and, when every round is full, at most a few percent more than the average;
+// the packed item table a launch reads holds every item once, and within a bin the four waves of each item (one per
+// SIMD) end up with tile totals that differ by at most one.
 // Prints "0 failure(s)" on success.
 #include <attention_plan.hpp>
 
+#include <cstdint>
 #include <cstdio>
 #include <vector>
 
@@ -35,6 +38,62 @@ static void check(const long long seqs, const int tiles, const int cus, const bo
             std::printf("FAIL seqs=%lld tiles=%d: an item is dealt %d times\n", seqs, tiles, h);
             ++failures;
             return;
+        }
+    }
+    // The item table a launch reads (fill_item_table) holds the same items, and within each bin the SPLIT = 4 waves
+    // of every item take its tiles from plan_lead: the per-sub totals (one SIMD each) differ by at most one tile.
+    const auto cost = [&](const int tile) { return causal ? tile + 1 : 1; };
+    const int heads = seqs % 3 == 0 ? 3 : 1;
+    std::vector<uint32_t> table(rk::kMaxTableItems, 0u);
+    const bool filled = rk::fill_item_table(table.data(), p, p.rounds, heads, cost);
+    const bool fits = static_cast<long long>(p.groups) * p.bins * p.rounds <= rk::kMaxTableItems;
+    if (filled != fits) {
+        std::printf("FAIL seqs=%lld tiles=%d: table filled=%d, expected %d\n", seqs, tiles, filled ? 1 : 0, fits ? 1 : 0);
+        ++failures;
+        return;
+    }
+    if (filled) {
+        std::vector<int> seen(static_cast<size_t>(seqs) * tiles, 0);
+        for (int g = 0; g < p.groups * p.bins; ++g) {
+            long long sub_tiles[4] = {0, 0, 0, 0};
+            for (int j = 0; j < p.rounds; ++j) {
+                const uint32_t e = table[static_cast<size_t>(g) * p.rounds + j];
+                if (e == rk::kNoItem) continue;
+                const int b = static_cast<int>(e & 1023u), head = static_cast<int>((e >> 10) & 1023u);
+                const int rank = static_cast<int>((e >> 20) & 1023u), rotation = static_cast<int>(e >> 30);
+                const int seq = b * heads + head;
+                const int tile = causal ? tiles - 1 - rank : rank;
+                if (head >= heads || seq >= seqs || rank >= tiles || seq % p.groups != g % p.groups) {
+                    std::printf("FAIL seqs=%lld tiles=%d: bad table entry %08x\n", seqs, tiles, e);
+                    ++failures;
+                    return;
+                }
+                ++seen[static_cast<size_t>(seq) * tiles + tile];
+                const int c = cost(tile);
+                for (int sub = 0; sub < 4; ++sub) {
+                    const int lead = rk::plan_lead(rotation, sub, 4);
+                    sub_tiles[sub] += c > lead ? (c - lead + 3) / 4 : 0;
+                }
+            }
+            long long lo = sub_tiles[0], hi = sub_tiles[0], sum = 0;
+            for (const long long t : sub_tiles) {
+                lo = t < lo ? t : lo;
+                hi = t > hi ? t : hi;
+                sum += t;
+            }
+            if (hi - lo > 1 || sum != load[g]) {
+                std::printf("FAIL seqs=%lld tiles=%d: bin %d sub tiles %lld..%lld (sum %lld, bin load %lld)\n", seqs, tiles, g, lo,
+                        hi, sum, load[g]);
+                ++failures;
+                return;
+            }
+        }
+        for (const int h : seen) {
+            if (h != 1) {
+                std::printf("FAIL seqs=%lld tiles=%d: the table holds an item %d times\n", seqs, tiles, h);
+                ++failures;
+                return;
+            }
         }
     }
     long long total = 0, most = 0;
