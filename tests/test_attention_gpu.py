@@ -271,6 +271,37 @@ def test_config5_64wide_radius256_causal(device):
     _subset_and_invariants(device, 64, 16, 8192, 256, mask, subset=2)
 
 
+# ---- persistent grid: item table, 2 or 3 items per CU, per-XCD or whole-chip bins -----------------------------
+
+@pytest.mark.parametrize("width,batch,heads,length,radius,causal,pad", [
+    (32, 1, 10, 1024, -1, True, False),   # 320 items: 2 per CU, 10 sequences (bins over the whole chip)
+    (32, 2, 8, 1536, -1, True, True),     # 768 items: 3 per CU, per-XCD bins, key padding
+    (32, 1, 20, 512, 100, False, False),  # 320 items, radius window without the causal mask
+    (64, 1, 8, 2048, -1, True, False),    # 512 items at d=64: 2 per CU
+    (64, 3, 3, 1024, 40, True, True),     # 288 items at d=64, radius and padding, 9 sequences
+])
+def test_persistent_grid_mappings(device, width, batch, heads, length, radius, causal, pad):
+    # On a 256-CU MI355X these shapes take the persistent forward (and, at d=32, the persistent dQ pass) with the
+    # host-built item table; the forward and backward must match the oracle as on every other path.
+    q, k, v, du = normal_case(700 + length + heads, width, batch, heads, length, length)
+    mask = padding_mask(705, batch, length, length // 2) if pad else np.ones((batch, length), np.uint8)
+    want = oracle.attention(q, k, v, mask, du, radius=radius, causal=causal)
+    out, lse, gq, gk, gv, delta = run_both(device, q, k, v, du, mask, radius=radius, causal=causal)
+    check_forward(out, lse, want)
+    check_backward(gq, gk, gv, delta, want)
+
+
+def test_persistent_grid_16_wide_generic_forward(device):
+    # 16 sequences x 32 tiles = 512 items at d=16: the generic forward's persistent path with 2 items per CU.
+    q, k, v, _ = normal_case(760, 16, 2, 8, 1024, 1024)
+    mask = padding_mask(761, 2, 1024, 600)
+    want = oracle.attention(q, k, v, mask, radius=-1, causal=False)
+    tq, tk, tv, tm = to_dev(device, q, k, v, mask)
+    out, lse = attention.generic_forward(tq, tk, tv, tm)
+    out, lse = host(out, lse)
+    check_forward(out, lse, want)
+
+
 # ---- edge cases ----------------------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("width", [32, 64])
