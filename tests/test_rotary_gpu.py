@@ -66,3 +66,21 @@ def test_rotary_strided_unaligned_and_broadcast_tables(device):
     hq, hk, hc, hs = (t.cpu().numpy() for t in (q, k, cos, sin))
     assert np.array_equal(oq.cpu().numpy(), oracle.rotary(hq, hc, hs))
     assert np.array_equal(ok.cpu().numpy(), oracle.rotary(hk, hc, hs))
+
+
+def test_rotary_backward_inverts_forward(device):
+    # With real angles shared by columns c and c + 16 (cos² + sin² = 1), the backward rotation is the inverse of the
+    # forward one: backward(forward(x)) = x up to rounding, at the config-2 shape.
+    batch, heads, length = 2, 12, 1024
+    x = torch.from_numpy(inputs.normal(60, (batch, heads, length, 32))).to(device)
+    theta = np.outer(np.arange(length), 1.0 / (10000.0 ** (np.arange(16) / 16.0)))
+    angles = np.concatenate([theta, theta], axis=1)[None].repeat(batch, axis=0)
+    cos = torch.from_numpy(np.cos(angles).astype(np.float32)).to(device)
+    sin = torch.from_numpy(np.sin(angles).astype(np.float32)).to(device)
+    yq, yk = attention.rotary(x, x, cos, sin)  # token-major [B][L][H][32]
+    y = yq.permute(0, 2, 1, 3)                  # back to [B][H][L][32] as a strided view
+    zq, zk = attention.rotary(y, y, cos, sin, backward=True)
+    torch.cuda.synchronize()
+    back = zq.permute(0, 2, 1, 3).cpu().numpy()
+    assert np.array_equal(yq.cpu().numpy(), yk.cpu().numpy()) and np.array_equal(zq.cpu().numpy(), zk.cpu().numpy())
+    assert np.abs(back - x.cpu().numpy()).max() <= 1e-5 * max(1.0, float(np.abs(x.cpu().numpy()).max()))
