@@ -285,9 +285,12 @@ __global__ __launch_bounds__(kThreads) void attention_dkdv_kernel(const Tensor q
     };
 
     // One query tile; the next tile's rows are loaded into the other set after the MFMAs are issued. q0 >= last
-    // marks the padding step of a wave with an odd number of tiles (the kernel has no masked-query skip: a
-    // padding step computes zeros).
+    // marks the padding step of a wave with an odd number of tiles: it only issues the next loads.
     auto step = [&](const Rows &r, const int q0, Rows &next, const int next_q0) __attribute__((always_inline)) {
+        if (q0 >= last) {
+            load_rows(next, next_q0);
+            return;
+        }
         // Per-query constants for the 32 queries of the tile, staged in this wave's LDS slice and read back in
         // accumulator order (lane needs queries q0 + tile_row(j, h)). Queries past the end get exp2(-inf) = 0.
         wave_lds_sync();
