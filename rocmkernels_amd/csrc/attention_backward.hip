@@ -191,10 +191,15 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
     for (int t = 0; t < DT; ++t) store_tile_row<VEC>(dst + 32 * t, acc[t], scale, h);
 }
 
-template<int D, bool VEC, int SPLIT, bool FUSED>
-__global__ __launch_bounds__(kThreads) void attention_dkdv_kernel(const Tensor q, const Tensor k, const Tensor v,
-        const uint8_t *__restrict__ mask, const float *__restrict__ lse, const Tensor du, const float *__restrict__ delta,
-        float *__restrict__ dk, float *__restrict__ dv, float *__restrict__ dq, const Shape s, const float scale) {
+// dK and dV contributions (and, FUSED, dQ, added with atomics) of key tile kt of sequence (b, head) over its query
+// tiles start, start + stride, ... (at most `limit` of them), accumulated into acc_k (dKᵀ without the 1/√D factor)
+// and acc_v (dVᵀ): accumulator register j of slice t is feature 32t + tile_row(j, h), lane%32 is key kt*32 + lane%32.
+// A key tile at or past the last key contributes nothing. WAVES = the workgroup's waves (one LDS slice each).
+template<int D, bool VEC, bool FUSED, int WAVES>
+__device__ __forceinline__ void dkdv_tiles(const Tensor &q, const Tensor &k, const Tensor &v, const uint8_t *__restrict__ mask,
+        const float *__restrict__ lse, const Tensor &du, const float *__restrict__ delta, float *__restrict__ dq, const Shape &s,
+        const float scale, const int b, const int head, const int kt, const int start, const int stride, const int limit,
+        f32x16 (&acc_k)[D / 32], f32x16 (&acc_v)[D / 32]) {
     constexpr int HALF = D / 2;
     constexpr int DT = D / 32;
 
@@ -203,43 +208,36 @@ __global__ __launch_bounds__(kThreads) void attention_dkdv_kernel(const Tensor q
     const int col = lane & 31;
     const int h = lane >> 5;
 
-    const int ktiles = (s.keys + kTile - 1) / kTile;
-    const WorkItem w = work_item<SPLIT>(s, ktiles);
-    const int key0 = w.rank * kTile; // under a causal mask the first key tiles see the most queries
+    const int seq = b * s.heads + head;
+    const int key0 = kt * kTile; // under a causal mask the first key tiles see the most queries
     const int key = key0 + col;
-    const bool in_range = w.valid && key < s.keys;
-    const Buffer mbuf = make_buffer(mask + static_cast<int64_t>(w.b) * s.keys, static_cast<uint32_t>(s.keys));
+    const bool in_range = key < s.keys;
+    const Buffer mbuf = make_buffer(mask + static_cast<int64_t>(b) * s.keys, static_cast<uint32_t>(s.keys));
     const bool visible = in_range && buffer_load_byte(mbuf, static_cast<uint32_t>(key)) != 0;
     const uint32_t bits = static_cast<uint32_t>(__ballot(visible));
     const float c2 = scale * kLog2e;
 
-    const Buffer kbuf = make_buffer(sequence(k, w.b, w.head), sequence_bytes(s.keys, k.st, D));
-    const Buffer vbuf = make_buffer(sequence(v, w.b, w.head), sequence_bytes(s.keys, v.st, D));
+    const Buffer kbuf = make_buffer(sequence(k, b, head), sequence_bytes(s.keys, k.st, D));
+    const Buffer vbuf = make_buffer(sequence(v, b, head), sequence_bytes(s.keys, v.st, D));
     float kr[HALF], vr[HALF];
     buffer_load_span<VEC>(kr, kbuf, in_range ? static_cast<uint32_t>(key) * (4u * k.st) + 4u * h * HALF : kNoRow);
     buffer_load_span<VEC>(vr, vbuf, in_range ? static_cast<uint32_t>(key) * (4u * v.st) + 4u * h * HALF : kNoRow);
 
-    int first = s.causal ? key0 : 0;
-    int last = s.queries;
-    if (s.radius >= 0) {
-        first = max(first, key0 - s.radius);
-        last = min(last, key0 + kTile + s.radius);
-    }
-    first = max(first, 0);
-    const int ntiles = (bits != 0 && last > first) ? (last - first + kTile - 1) / kTile : 0;
+    int first, last;
+    const int range = dkdv_query_range(s, kt, first, last);
+    const int ntiles = bits != 0 ? range : 0;
     // Queries that see this lane's key: [qlo, qhi] (also capped at the last query of the range).
     const int qlo = window_query_lo(s, key);
     const int qhi = min(window_query_hi(s, key), last - 1);
 
-
-    const Buffer qbuf = make_buffer(sequence(q, w.b, w.head), sequence_bytes(s.queries, q.st, D));
-    const Buffer ubuf = make_buffer(sequence(du, w.b, w.head), sequence_bytes(s.queries, du.st, D));
-    const Buffer lbuf = make_buffer(lse + static_cast<int64_t>(w.seq) * s.queries * 2, static_cast<uint32_t>(s.queries) * 8u);
-    const Buffer dbuf = make_buffer(delta + static_cast<int64_t>(w.seq) * s.queries, static_cast<uint32_t>(s.queries) * 4u);
+    const Buffer qbuf = make_buffer(sequence(q, b, head), sequence_bytes(s.queries, q.st, D));
+    const Buffer ubuf = make_buffer(sequence(du, b, head), sequence_bytes(s.queries, du.st, D));
+    const Buffer lbuf = make_buffer(lse + static_cast<int64_t>(seq) * s.queries * 2, static_cast<uint32_t>(s.queries) * 8u);
+    const Buffer dbuf = make_buffer(delta + static_cast<int64_t>(seq) * s.queries, static_cast<uint32_t>(s.queries) * 4u);
     const uint32_t qstep = 4u * q.st;
     const uint32_t ustep = 4u * du.st;
 
-    __shared__ __align__(16) float stats[kWaves][2][kTile];
+    __shared__ __align__(16) float stats[WAVES][2][kTile];
 
     // Fused dQ: K of this item in column layout (the B operand of dQ = dS·K, row key0 + tile_row(j, h), feature
     // 32t + col), pre-scaled by 1/√D and zero for masked keys, whatever K holds there. dS goes through the
@@ -248,8 +246,8 @@ __global__ __launch_bounds__(kThreads) void attention_dkdv_kernel(const Tensor q
     // resource and are dropped by the hardware.
     constexpr int KC = FUSED ? DT : 0;
     float kq[KC > 0 ? KC : 1][16];
-    __shared__ __align__(16) float dsl[FUSED ? kWaves : 1][kTile][kTile + 4];
-    const Buffer qgbuf = make_buffer(dq + static_cast<int64_t>(w.seq) * s.queries * D, FUSED ? static_cast<uint32_t>(s.queries) * (4u * D) : 0u);
+    __shared__ __align__(16) float dsl[FUSED ? WAVES : 1][kTile][kTile + 4];
+    const Buffer qgbuf = make_buffer(dq + static_cast<int64_t>(seq) * s.queries * D, FUSED ? static_cast<uint32_t>(s.queries) * (4u * D) : 0u);
     if constexpr (FUSED) {
         const uint32_t klane = static_cast<uint32_t>(key0 + 4 * h) * (4u * k.st) + 4u * col;
 #pragma unroll
@@ -263,7 +261,6 @@ __global__ __launch_bounds__(kThreads) void attention_dkdv_kernel(const Tensor q
         }
     }
 
-    f32x16 acc_k[DT], acc_v[DT];
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
         acc_k[t] = f32x16{};
@@ -284,10 +281,10 @@ __global__ __launch_bounds__(kThreads) void attention_dkdv_kernel(const Tensor q
         r.d = buffer_load(dbuf, qq * 4u, 0);
     };
 
-    // One query tile; the next tile's rows are loaded into the other set after the MFMAs are issued. q0 >= last
-    // marks the padding step of a wave with an odd number of tiles: it only issues the next loads.
-    auto step = [&](const Rows &r, const int q0, Rows &next, const int next_q0) __attribute__((always_inline)) {
-        if (q0 >= last) {
+    // One query tile; the next tile's rows are loaded into the other set after the MFMAs are issued. An inactive
+    // step (the padding step of a wave with an odd number of tiles) only issues the next loads.
+    auto step = [&](const Rows &r, const int q0, const bool active, Rows &next, const int next_q0) __attribute__((always_inline)) {
+        if (!active) {
             load_rows(next, next_q0);
             return;
         }
@@ -354,7 +351,7 @@ __global__ __launch_bounds__(kThreads) void attention_dkdv_kernel(const Tensor q
                 acc_k[t] = mfma(qc[t][j], dp[j], acc_k[t]);
             }
         }
-        if (FUSED && q0 < last) {
+        if constexpr (FUSED) {
             // dS (keys on lanes) → LDS [query][key] → queries on lanes: A operand of dQ MFMA j is
             // dS[q0 + col][key0 + tile_row(j, h)], four consecutive keys per 128-bit read.
 #pragma unroll
@@ -385,19 +382,35 @@ __global__ __launch_bounds__(kThreads) void attention_dkdv_kernel(const Tensor q
         }
     };
 
-    // Tiles lead, lead + SPLIT, ...; the count is rounded up to even so the loop body is two straight-line steps.
-    const int mine = ntiles > w.lead ? (ntiles - w.lead + SPLIT - 1) / SPLIT : 0;
+    // Tiles start, start + stride, ...; the count is rounded up to even so the loop body is two straight-line steps.
+    const int mine = ntiles > start ? min(limit, (ntiles - start + stride - 1) / stride) : 0;
     Rows ra, rb;
-    if (mine > 0) load_rows(ra, first + w.lead * kTile);
+    if (mine > 0) load_rows(ra, first + start * kTile);
     for (int i = 0; i < mine; i += 2) {
-        const int q0 = first + (w.lead + i * SPLIT) * kTile;
-        step(ra, q0, rb, q0 + SPLIT * kTile);
-        step(rb, q0 + SPLIT * kTile, ra, q0 + 2 * SPLIT * kTile);
+        const int q0 = first + (start + i * stride) * kTile;
+        step(ra, q0, true, rb, q0 + stride * kTile);
+        step(rb, q0 + stride * kTile, i + 1 < mine, ra, q0 + 2 * stride * kTile);
     }
+}
+
+template<int D, bool VEC, int SPLIT, bool FUSED>
+__global__ __launch_bounds__(kThreads) void attention_dkdv_kernel(const Tensor q, const Tensor k, const Tensor v,
+        const uint8_t *__restrict__ mask, const float *__restrict__ lse, const Tensor du, const float *__restrict__ delta,
+        float *__restrict__ dk, float *__restrict__ dv, float *__restrict__ dq, const Shape s, const float scale) {
+    constexpr int DT = D / 32;
+    const int col = threadIdx.x & 31;
+    const int h = (threadIdx.x >> 5) & 1;
+    const int ktiles = (s.keys + kTile - 1) / kTile;
+    const WorkItem w = work_item<SPLIT>(s, ktiles);
+    const int kt = w.valid ? w.rank : ktiles; // past the last key tile: no work
+    f32x16 acc_k[DT], acc_v[DT];
+    dkdv_tiles<D, VEC, FUSED, kWaves>(q, k, v, mask, lse, du, delta, dq, s, scale, w.b, w.head, kt, w.lead, SPLIT, 0x7fffffff,
+            acc_k, acc_v);
 
     split_sum<SPLIT>(acc_k, w.sub);
     split_sum<SPLIT>(acc_v, w.sub);
-    if (w.sub != 0 || !in_range) return;
+    const int key = kt * kTile + col;
+    if (w.sub != 0 || key >= s.keys) return;
     const int64_t krow = (static_cast<int64_t>(w.seq) * s.keys + key) * D;
 #pragma unroll
     for (int t = 0; t < DT; ++t) {

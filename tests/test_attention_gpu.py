@@ -424,6 +424,10 @@ def run_fused_and_default(device, q, k, v, du, mask, radius, causal):
     (64, 1, 2, 90, 50, -1, False, True),
     (64, 2, 1, 64, 200, -1, True, False),
     (64, 1, 3, 5, 7, 2, False, False),
+    (32, 4, 5, 40, 40, -1, True, True),     # 20 short sequences, two key tiles each
+    (32, 2, 4, 64, 64, -1, True, False),
+    (64, 2, 4, 100, 100, 9, True, True),    # radius and padding at d=64
+    (32, 1, 2, 40, 200, 5, False, False),   # key tiles past query 45 see no query: their dK/dV are zero
 ])
 def test_fused_backward_matches_oracle(device, width, batch, heads, queries, keys, radius, causal, pad):
     q, k, v, du = normal_case(700 + queries + keys, width, batch, heads, queries, keys)
