@@ -195,7 +195,18 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
 // tiles start, start + stride, ... (at most `limit` of them), accumulated into acc_k (dKᵀ without the 1/√D factor)
 // and acc_v (dVᵀ): accumulator register j of slice t is feature 32t + tile_row(j, h), lane%32 is key kt*32 + lane%32.
 // A key tile at or past the last key contributes nothing. WAVES = the workgroup's waves (one LDS slice each).
-template<int D, bool VEC, bool FUSED, int WAVES>
+// STAGE (128-bit access only): each Q and dO tile is loaded a whole line per request and staged through this wave's
+// LDS slots, from which the wave reads both the row layout (S and dP operands) and the column layout (dK and dV
+// operands); one register set of raw rows is carried a tile ahead. That needs about 70 fewer registers than the row
+// spans plus column loads (two sets of rows in flight), enough for three waves per SIMD at D = 32.
+// LDS slots of the staged dK/dV path: a Q tile and a dO tile per wave.
+template<int D, int WAVES>
+__device__ __forceinline__ float *dkdv_slots() {
+    __shared__ __align__(16) float slots[WAVES * 2 * kSlotFloats<D>];
+    return slots;
+}
+
+template<int D, bool VEC, bool FUSED, int WAVES, bool STAGE = false>
 __device__ __forceinline__ void dkdv_tiles(const Tensor &q, const Tensor &k, const Tensor &v, const uint8_t *__restrict__ mask,
         const float *__restrict__ lse, const Tensor &du, const float *__restrict__ delta, float *__restrict__ dq, const Shape &s,
         const float scale, const int b, const int head, const int kt, const int start, const int stride, const int limit,
@@ -382,33 +393,154 @@ __device__ __forceinline__ void dkdv_tiles(const Tensor &q, const Tensor &k, con
         }
     };
 
-    // Tiles start, start + stride, ...; the count is rounded up to even so the loop body is two straight-line steps.
     const int mine = ntiles > start ? min(limit, (ntiles - start + stride - 1) / stride) : 0;
-    Rows ra, rb;
-    if (mine > 0) load_rows(ra, first + start * kTile);
-    for (int i = 0; i < mine; i += 2) {
-        const int q0 = first + (start + i * stride) * kTile;
-        step(ra, q0, true, rb, q0 + stride * kTile);
-        step(rb, q0 + stride * kTile, i + 1 < mine, ra, q0 + 2 * stride * kTile);
+    if constexpr (STAGE) {
+        static_assert(VEC, "staged tiles need 128-bit access");
+        float *const qslot = dkdv_slots<D, WAVES>() + 2 * wave * kSlotFloats<D>;
+        float *const uslot = qslot + kSlotFloats<D>;
+        // Raw Q and dO rows and the softmax statistics of one query tile, loaded a tile ahead.
+        struct Raw {
+            RowTile<D> q;
+            float m, l, d;
+        };
+        auto load_raw = [&](Raw &r, const int q0) __attribute__((always_inline)) {
+            load_row_tile<D>(r.q, qbuf, qstep, static_cast<uint32_t>(q0) * qstep);
+            const uint32_t qq = static_cast<uint32_t>(q0 + col);
+            r.m = buffer_load(lbuf, qq * 8u, 0);
+            r.l = buffer_load(lbuf, qq * 8u + 4u, 0);
+            r.d = buffer_load(dbuf, qq * 4u, 0);
+        };
+        // One query tile: stage r, then load the next tile's rows into r while this one computes.
+        auto stage_step = [&](Raw &r, const int q0, const int next_q0) __attribute__((always_inline)) {
+            wave_lds_sync();
+            if (h == 0) {
+                const bool ok = q0 + col < last && r.m != -INFINITY;
+                stats[wave][0][col] = ok ? fmaf(r.m, kLog2e, __log2f(r.l)) : INFINITY; // exp2(s·c2 - this) = P
+                stats[wave][1][col] = r.d;
+            }
+            {
+                RowTile<D> u;
+                load_row_tile<D>(u, ubuf, ustep, static_cast<uint32_t>(q0) * ustep);
+                write_row_tile<D>(qslot, r.q);
+                write_row_tile<D>(uslot, u);
+            }
+            wave_lds_sync();
+            load_raw(r, next_q0);
+
+            f32x16 sc{}, dp{};
+            {
+                float qr[HALF];
+                read_row_layout<D>(qslot, qr);
+#pragma unroll
+                for (int c = 0; c < HALF; ++c) sc = mfma(qr[c], kr[c], sc);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            {
+                float ur[HALF];
+                read_row_layout<D>(uslot, ur);
+#pragma unroll
+                for (int c = 0; c < HALF; ++c) dp = mfma(ur[c], vr[c], dp);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+
+            // Four rows' constants at a time (all sixteen at once would hold 24 more registers).
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                __builtin_amdgcn_sched_barrier(0);
+                const f32x4 mcs = *reinterpret_cast<const f32x4 *>(&stats[wave][0][8 * u + 4 * h]);
+                const f32x4 dls = *reinterpret_cast<const f32x4 *>(&stats[wave][1][8 * u + 4 * h]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int j = 4 * u + i;
+                    const float p = exp2_fast(fmaf(sc[j], c2, -mcs[i]));
+                    sc[j] = p;
+                    dp[j] = p * (dp[j] - dls[i]);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (bits != 0xffffffffu || q0 + kTile > last || !tile_in_window(s, q0, key0)) {
+                const uint32_t keep = visible ? bit_range(qlo - q0, qhi - q0) >> (4 * h) : 0u;
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const bool ok = (keep >> (8 * (j >> 2) + (j & 3))) & 1u;
+                    sc[j] = ok ? sc[j] : 0.0f;
+                    dp[j] = ok ? dp[j] : 0.0f;
+                }
+            }
+            // Column layouts eight rows at a time: all of both at once would hold 48 * D / 32 more registers.
+            auto column_product = [&](const float *slot, const f32x16 &b, f32x16 (&acc)[DT]) __attribute__((always_inline)) {
+                __builtin_amdgcn_sched_barrier(0);
+                {
+                    float c[DT][8];
+                    read_column_layout<D, 0, 8>(slot, c);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+#pragma unroll
+                        for (int t = 0; t < DT; ++t) acc[t] = mfma(c[t][j], b[j], acc[t]);
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                {
+                    float c[DT][8];
+                    read_column_layout<D, 8, 8>(slot, c);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+#pragma unroll
+                        for (int t = 0; t < DT; ++t) acc[t] = mfma(c[t][j], b[8 + j], acc[t]);
+                    }
+                }
+            };
+            column_product(uslot, sc, acc_v);
+            column_product(qslot, dp, acc_k);
+        };
+        Raw r;
+        if (mine > 0) load_raw(r, first + start * kTile);
+        for (int i = 0; i < mine; ++i) {
+            const int q0 = first + (start + i * stride) * kTile;
+            stage_step(r, q0, q0 + stride * kTile);
+        }
+    } else {
+        // Tiles start, start + stride, ...; the count is rounded up to even so the loop body is two straight-line
+        // steps.
+        Rows ra, rb;
+        if (mine > 0) load_rows(ra, first + start * kTile);
+        for (int i = 0; i < mine; i += 2) {
+            const int q0 = first + (start + i * stride) * kTile;
+            step(ra, q0, true, rb, q0 + stride * kTile);
+            step(rb, q0 + stride * kTile, i + 1 < mine, ra, q0 + 2 * stride * kTile);
+        }
     }
 }
 
-template<int D, bool VEC, int SPLIT, bool FUSED>
-__global__ __launch_bounds__(kThreads) void attention_dkdv_kernel(const Tensor q, const Tensor k, const Tensor v,
-        const uint8_t *__restrict__ mask, const float *__restrict__ lse, const Tensor du, const float *__restrict__ delta,
-        float *__restrict__ dk, float *__restrict__ dv, float *__restrict__ dq, const Shape s, const float scale) {
+// NI = 0: items (key tiles) in dispatch order, 4-wave workgroups; NI > 0: persistent grid of NI * SPLIT-wave workgroups
+// taking the NI items of their bin from the launch's item table (staged Q/dO tiles, see dkdv_tiles), as in the forward.
+template<int D, bool VEC, int SPLIT, bool FUSED, int NI = 0>
+__global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attention_dkdv_kernel(const Tensor q, const Tensor k,
+        const Tensor v, const uint8_t *__restrict__ mask, const float *__restrict__ lse, const Tensor du,
+        const float *__restrict__ delta, float *__restrict__ dk, float *__restrict__ dv, float *__restrict__ dq, const Shape s,
+        const ItemTable<NI> items, const float scale) {
     constexpr int DT = D / 32;
+    constexpr int WG = NI > 0 ? NI * SPLIT : kWaves;
     const int col = threadIdx.x & 31;
     const int h = (threadIdx.x >> 5) & 1;
     const int ktiles = (s.keys + kTile - 1) / kTile;
-    const WorkItem w = work_item<SPLIT>(s, ktiles);
+    const WorkItem w = [&] {
+        if constexpr (NI > 0) return planned_item<SPLIT, NI>(s, items);
+        else return work_item<SPLIT>(s, ktiles);
+    }();
     const int kt = w.valid ? w.rank : ktiles; // past the last key tile: no work
     f32x16 acc_k[DT], acc_v[DT];
-    dkdv_tiles<D, VEC, FUSED, kWaves>(q, k, v, mask, lse, du, delta, dq, s, scale, w.b, w.head, kt, w.lead, SPLIT, 0x7fffffff,
-            acc_k, acc_v);
+    dkdv_tiles<D, VEC, FUSED, WG, (NI > 0)>(q, k, v, mask, lse, du, delta, dq, s, scale, w.b, w.head, kt, w.lead, SPLIT,
+            0x7fffffff, acc_k, acc_v);
 
-    split_sum<SPLIT>(acc_k, w.sub);
-    split_sum<SPLIT>(acc_v, w.sub);
+    if constexpr (NI > 0) { // the staged path's LDS slots are free once every wave has left its loop
+        static_assert(WG * 16 * DT * kWave <= WG * 2 * kSlotFloats<D>);
+        split_sum_into<SPLIT, DT, WG>(acc_k, w.sub, dkdv_slots<D, WG>());
+        split_sum_into<SPLIT, DT, WG>(acc_v, w.sub, dkdv_slots<D, WG>());
+    } else {
+        split_sum<SPLIT, DT, WG>(acc_k, w.sub);
+        split_sum<SPLIT, DT, WG>(acc_v, w.sub);
+    }
     const int key = kt * kTile + col;
     if (w.sub != 0 || key >= s.keys) return;
     const int64_t krow = (static_cast<int64_t>(w.seq) * s.keys + key) * D;
@@ -467,14 +599,16 @@ void launch_dq_mapped(const BackwardArgs &a, const int cus, hipStream_t stream) 
     else launch_dq<D, MODE, VEC, 4>(a, stream);
 }
 
-template<int D, bool VEC, int SPLIT, bool FUSED>
-void launch_dkdv(const BackwardArgs &a, hipStream_t stream) {
+template<int D, bool VEC, int SPLIT, bool FUSED, int NI = 0>
+void launch_dkdv(const BackwardArgs &a, hipStream_t stream, const unsigned planned_grid = 0, const ItemTable<NI> &table = ItemTable<NI>{}) {
     const Shape shape{a.batch, a.heads, a.queries, a.keys, a.radius, a.causal};
     const float scale = 1.0f / sqrtf(static_cast<float>(D));
     const int64_t items = static_cast<int64_t>((a.keys + kTile - 1) / kTile) * a.batch * a.heads;
-    hipLaunchKernelGGL((attention_dkdv_kernel<D, VEC, SPLIT, FUSED>), dim3(workgroups_for(items, SPLIT)), dim3(kThreads), 0, stream,
-            tensor(a.q, a.qs), tensor(a.k, a.ks), tensor(a.v, a.vs), reinterpret_cast<const uint8_t *>(a.mask), a.lse,
-            tensor(a.upstream, a.us), a.delta, a.gradient_k, a.gradient_v, a.gradient_q, shape, scale);
+    const unsigned grid = NI > 0 ? planned_grid : workgroups_for(items, SPLIT);
+    const unsigned threads = kWave * (NI > 0 ? NI * SPLIT : kWaves);
+    hipLaunchKernelGGL((attention_dkdv_kernel<D, VEC, SPLIT, FUSED, NI>), dim3(grid), dim3(threads), 0, stream, tensor(a.q, a.qs),
+            tensor(a.k, a.ks), tensor(a.v, a.vs), reinterpret_cast<const uint8_t *>(a.mask), a.lse, tensor(a.upstream, a.us), a.delta,
+            a.gradient_k, a.gradient_v, a.gradient_q, shape, table, scale);
 }
 
 template<int D, bool VEC, bool FUSED>
@@ -482,6 +616,32 @@ void launch_dkdv_split(const BackwardArgs &a, const int split, hipStream_t strea
     if (split == 1) launch_dkdv<D, VEC, 1, FUSED>(a, stream);
     else if (split == 2) launch_dkdv<D, VEC, 2, FUSED>(a, stream);
     else launch_dkdv<D, VEC, 4, FUSED>(a, stream);
+}
+
+// Deterministic dK/dV pass. At d=32 with 128-bit access (staged Q/dO tiles: about 150 VGPRs, 3 waves per SIMD) and
+// more key tiles than CUs but no more than 3 per CU, a persistent cost-balanced grid as in the forward; otherwise
+// SPLIT waves per key tile in dispatch order.
+template<int D, bool VEC>
+void launch_dkdv_mapped(const BackwardArgs &a, const int cus, hipStream_t stream) {
+    const int ktiles = (a.keys + kTile - 1) / kTile;
+    const int64_t items = static_cast<int64_t>(ktiles) * a.batch * a.heads;
+    if constexpr (D == 32 && VEC) {
+        if (items > cus && items <= 3ll * cus) {
+            const Shape shape{a.batch, a.heads, a.queries, a.keys, a.radius, a.causal};
+            const Plan plan = make_plan(static_cast<int64_t>(a.batch) * a.heads, ktiles, cus, false); // key tile 0 first
+            const unsigned grid = static_cast<unsigned>(plan.groups * plan.bins);
+            if (plan.rounds == 3) {
+                if (const ItemTable<3> *table = item_table<3, true>(shape, plan)) {
+                    launch_dkdv<D, VEC, 4, false, 3>(a, stream, grid, *table);
+                    return;
+                }
+            } else if (const ItemTable<2> *table = item_table<2, true>(shape, plan)) {
+                launch_dkdv<D, VEC, 4, false, 2>(a, stream, grid, *table);
+                return;
+            }
+        }
+    }
+    launch_dkdv_split<D, VEC, false>(a, backward_split_for(items), stream);
 }
 
 
@@ -502,7 +662,7 @@ hipError_t run(const BackwardStage stage, const BackwardArgs &a, const int cus, 
         const hipError_t error = hipGetLastError();
         if (error != hipSuccess || stage != kBackwardAll) return error;
     }
-    launch_dkdv_split<D, VEC, false>(a, backward_split_for(kitems), stream);
+    launch_dkdv_mapped<D, VEC>(a, cus, stream);
     return hipGetLastError();
 }
 

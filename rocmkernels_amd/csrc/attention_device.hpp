@@ -182,20 +182,19 @@ __device__ __forceinline__ void wave_lds_sync() {
 // those scattered requests queue up: the last waves of a CU received their first tile 3.4 us after launch against
 // 1.6 us for loads that cover whole lines (12 waves per CU, 12 KiB each). So a 32-row tile is read with loads that
 // cover whole lines (load i, lane L: 16-byte chunk i*64 + L of the tile in row-major order), written to the wave's
-// LDS slot and read back in row layout. Chunk c of row r is stored at chunk position c ^ row_swizzle(r), which keeps
-// the writes and the row-layout reads free of LDS bank conflicts (for 8-lane phases over 32 banks and for 16-lane
-// phases over 64 banks alike).
+// LDS slot and read back in row layout (or, for products that reduce over the tile's rows, in column layout). Slot
+// rows are D + 4 floats apart: the row-layout reads (lane%32 = row, 16 bytes each) and the column-layout reads (a
+// half-wave reads 32 consecutive floats of one row) then meet no bank conflict over 32 banks, and every address is
+// one per-lane base plus a constant.
+template<int D>
+constexpr int kSlotStride = D + 4;
+template<int D>
+constexpr int kSlotFloats = kTile * kSlotStride<D>;
+
 template<int D>
 struct RowTile {
     f32x4 x[D / 8]; // the tile's 32 * D floats, 16 bytes per lane per load
 };
-
-template<int D>
-__device__ __forceinline__ constexpr int row_swizzle(const int r) {
-    if constexpr (D == 64) return r & 15;
-    else if constexpr (D == 32) return (r & 7) ^ ((r >> 3) & 1);
-    else return ((r >> 1) ^ (r >> 2)) & 3;
-}
 
 // Issues the loads of the 32 rows that start at byte offset row0 of b, rows `step` bytes apart (rows at or beyond
 // the buffer's extent read 0: the range check covers voffset + soffset).
@@ -209,30 +208,54 @@ __device__ __forceinline__ void load_row_tile(RowTile<D> &t, const Buffer b, con
     for (int i = 0; i < D / 8; ++i) t.x[i] = buffer_load4(b, voffset, row0 + static_cast<uint32_t>(i * RPL) * step);
 }
 
-// Passes a loaded tile through the wave's LDS slot (32 * D floats, 16-byte aligned) into row layout: lane
-// (col, h) receives features h*D/2 .. h*D/2 + D/2 - 1 of row col.
+// Writes a loaded tile to the wave's LDS slot (kSlotFloats<D> floats, 16-byte aligned), after the slot's previous
+// reads.
 template<int D>
-__device__ __forceinline__ void stage_row_tile(float *slot, const RowTile<D> &t, float (&r)[D / 2]) {
+__device__ __forceinline__ void write_row_tile(float *slot, const RowTile<D> &t) {
     constexpr int CPR = D / 4;
     constexpr int RPL = kWave / CPR;
     const int lane = threadIdx.x & (kWave - 1);
-    const int col = lane & 31;
-    const int h = lane >> 5;
-    wave_lds_sync(); // the previous tile's row-layout reads come first
+    float *base = slot + (lane / CPR) * kSlotStride<D> + 4 * (lane % CPR);
+    wave_lds_sync(); // the previous tile's reads come first
 #pragma unroll
-    for (int i = 0; i < D / 8; ++i) {
-        const int row = i * RPL + lane / CPR;
-        *reinterpret_cast<f32x4 *>(slot + row * D + 4 * ((lane % CPR) ^ row_swizzle<D>(row))) = t.x[i];
-    }
-    wave_lds_sync();
+    for (int i = 0; i < D / 8; ++i) *reinterpret_cast<f32x4 *>(base + i * RPL * kSlotStride<D>) = t.x[i];
+}
+
+// Row layout from a written slot: lane (col, h) receives features h*D/2 .. h*D/2 + D/2 - 1 of row col. Call
+// wave_lds_sync() between the write and the first read.
+template<int D>
+__device__ __forceinline__ void read_row_layout(const float *slot, float (&r)[D / 2]) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const float *base = slot + (lane & 31) * kSlotStride<D> + (lane >> 5) * (D / 2);
 #pragma unroll
-    for (int k = 0; k < CPR / 2; ++k) {
-        const f32x4 x = *reinterpret_cast<const f32x4 *>(slot + col * D + 4 * ((h * (CPR / 2) + k) ^ row_swizzle<D>(col)));
+    for (int k = 0; k < D / 8; ++k) {
+        const f32x4 x = *reinterpret_cast<const f32x4 *>(base + 4 * k);
         r[4 * k + 0] = x[0];
         r[4 * k + 1] = x[1];
         r[4 * k + 2] = x[2];
         r[4 * k + 3] = x[3];
     }
+}
+
+// Column layout from a written slot: element [tile_row(j, h)][32t + col] to c[t][j - J0] for j = J0 .. J0 + J - 1 (the
+// A operands of MFMAs j of a product that reduces over the slot's rows).
+template<int D, int J0 = 0, int J = 16>
+__device__ __forceinline__ void read_column_layout(const float *slot, float (&c)[D / 32][J]) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const float *base = slot + 4 * (lane >> 5) * kSlotStride<D> + (lane & 31);
+#pragma unroll
+    for (int j = J0; j < J0 + J; ++j) {
+#pragma unroll
+        for (int t = 0; t < D / 32; ++t) c[t][j - J0] = base[(8 * (j >> 2) + (j & 3)) * kSlotStride<D> + 32 * t];
+    }
+}
+
+// Passes a loaded tile through the wave's LDS slot into row layout (write_row_tile, then read_row_layout).
+template<int D>
+__device__ __forceinline__ void stage_row_tile(float *slot, const RowTile<D> &t, float (&r)[D / 2]) {
+    write_row_tile<D>(slot, t);
+    wave_lds_sync();
+    read_row_layout<D>(slot, r);
 }
 
 // Keys [first, last) cover every key the 32 queries of query tile qt can see through the causal and radius windows;
@@ -336,9 +359,10 @@ __device__ __forceinline__ WorkItem planned_item(const Shape &s, const ItemTable
     return w;
 }
 
-// Host: the item table of a planned launch over shape s (forward and dQ items: 32-query tiles), or null when the
-// launch does not fit one. Kept per host thread for the last shape, so repeated launches do not rebuild it.
-template<int NI>
+// Host: the item table of a planned launch over shape s, or null when the launch does not fit one. Items are
+// 32-query tiles (forward and dQ; KEY_ITEMS false) or 32-key tiles (dK/dV). Kept per host thread for the last
+// shape, so repeated launches do not rebuild it.
+template<int NI, bool KEY_ITEMS = false>
 inline const ItemTable<NI> *item_table(const Shape &s, const Plan &p) {
     struct Cache {
         Shape s;
@@ -352,7 +376,10 @@ inline const ItemTable<NI> *item_table(const Shape &s, const Plan &p) {
             cache.p.bins == p.bins && cache.p.seqs == p.seqs && cache.p.tiles == p.tiles && cache.p.rounds == p.rounds &&
             cache.p.reverse == p.reverse;
     if (!same) {
-        cache.ok = fill_item_table(cache.table.entry, p, NI, s.heads, [&](const int tile) { return forward_item_tiles(s, tile); });
+        cache.ok = fill_item_table(cache.table.entry, p, NI, s.heads, [&](const int tile) {
+            int first, last;
+            return KEY_ITEMS ? dkdv_query_range(s, tile, first, last) : forward_item_tiles(s, tile);
+        });
         cache.s = s;
         cache.p = p;
     }
@@ -360,19 +387,20 @@ inline const ItemTable<NI> *item_table(const Shape &s, const Plan &p) {
 }
 
 // Sums accumulator tiles over the SPLIT waves of an item through LDS; the wave with sub == 0 ends with the total.
-// Every wave of the WG-wave workgroup must call it (it contains a workgroup barrier when SPLIT > 1).
-template<int SPLIT, int N, int WG = kWaves>
-__device__ __forceinline__ void split_sum(f32x16 (&acc)[N], const int sub) {
+// Every wave of the WG-wave workgroup must call it (it contains workgroup barriers when SPLIT > 1). `buffer` holds
+// WG * 16 * N * 64 floats; the first barrier also orders it after the workgroup's earlier uses of that memory.
+template<int SPLIT, int N, int WG>
+__device__ __forceinline__ void split_sum_into(f32x16 (&acc)[N], const int sub, float *buffer) {
     if constexpr (SPLIT > 1) {
-        __shared__ float partial[WG][16 * N][kWave];
         const int lane = threadIdx.x & (kWave - 1);
         const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave); // wave-uniform: keeps tile bookkeeping scalar
-        __syncthreads(); // a previous call with the same N may still be reading `partial`
+        float *mine = buffer + wave * (16 * N * kWave) + lane;
+        __syncthreads(); // a previous call, or the streaming loops, may still be reading this memory
         if (sub > 0) {
 #pragma unroll
             for (int t = 0; t < N; ++t) {
 #pragma unroll
-                for (int j = 0; j < 16; ++j) partial[wave][16 * t + j][lane] = acc[t][j];
+                for (int j = 0; j < 16; ++j) mine[(16 * t + j) * kWave] = acc[t][j];
             }
         }
         __syncthreads();
@@ -382,10 +410,18 @@ __device__ __forceinline__ void split_sum(f32x16 (&acc)[N], const int sub) {
 #pragma unroll
                 for (int t = 0; t < N; ++t) {
 #pragma unroll
-                    for (int j = 0; j < 16; ++j) acc[t][j] += partial[wave + w][16 * t + j][lane];
+                    for (int j = 0; j < 16; ++j) acc[t][j] += mine[w * (16 * N * kWave) + (16 * t + j) * kWave];
                 }
             }
         }
+    }
+}
+
+template<int SPLIT, int N, int WG = kWaves>
+__device__ __forceinline__ void split_sum(f32x16 (&acc)[N], const int sub) {
+    if constexpr (SPLIT > 1) {
+        __shared__ float partial[WG * 16 * N * kWave];
+        split_sum_into<SPLIT, N, WG>(acc, sub, partial);
     }
 }
 

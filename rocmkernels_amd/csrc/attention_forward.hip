@@ -73,7 +73,7 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
     // request and staged through this wave's LDS slot; otherwise each lane reads its own row span. (At D = 64 the
     // staged K tile pushes the kernel past the 256 registers that two waves per SIMD allow.)
     constexpr bool STAGE_K = VEC && D <= 32;
-    __shared__ __align__(16) float row_slots[VEC ? WG : 1][VEC ? kTile * D : 1];
+    __shared__ __align__(16) float row_slots[VEC ? WG : 1][VEC ? kSlotFloats<D> : 1];
     float *const slot = row_slots[VEC ? wave : 0];
     float qr[HALF];
     RowTile<D> qraw;
