@@ -53,10 +53,50 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
     const int64_t row = static_cast<int64_t>(w.seq) * s.queries + query;
     const float c2 = scale * kLog2e;
 
+    int first, last;
+    const int ntiles = w.valid ? forward_key_range(s, qt, first, last) : 0;
+    const int mine = ntiles > w.lead ? (ntiles - w.lead + SPLIT - 1) / SPLIT : 0;
+    const Buffer kbuf = make_buffer(sequence(k, w.b, w.head), sequence_bytes(s.keys, k.st, D));
+    const Buffer vbuf = make_buffer(sequence(v, w.b, w.head), sequence_bytes(s.keys, v.st, D));
+    const Buffer mbuf = make_buffer(mask + static_cast<int64_t>(w.b) * s.keys, static_cast<uint32_t>(s.keys));
+    const uint32_t kstep = 4u * k.st;
+    const uint32_t vstep = 4u * v.st;
+
+    // Persistent grid with 128-bit access: each K and V tile is loaded a whole line per request and staged through
+    // this wave's LDS slots, which give the row layouts (Sᵀ, dPᵀ operands) and K's column layout (dQᵀ operand). The
+    // first tile's loads go out before the query row's, so a wave waits for memory once before its first tile
+    // (issued after delta, they arrived 3-9 us after launch at the 24 x 1024 causal shape).
+    constexpr bool STAGE = NI > 0 && VEC && (MODE == kDqAndDelta || MODE == kDqFromDelta);
+    struct Raw {
+        RowTile<D> k, v;
+        int mask;
+    };
+    auto load_raw = [&](Raw &r, const int key0) __attribute__((always_inline)) {
+        r.mask = buffer_load_byte(mbuf, static_cast<uint32_t>(key0 + col)); // keys >= s.keys read 0: masked
+        load_row_tile<D>(r.k, kbuf, kstep, static_cast<uint32_t>(key0) * kstep);
+        load_row_tile<D>(r.v, vbuf, vstep, static_cast<uint32_t>(key0) * vstep);
+    };
+    Raw raw;
+    if constexpr (STAGE) {
+        if (mine > 0) load_raw(raw, first + w.lead * kTile);
+    }
+
     const Buffer ubuf = make_buffer(sequence(du, w.b, w.head), sequence_bytes(s.queries, du.st, D));
     const uint32_t qoff = static_cast<uint32_t>(query) * (4u * du.st) + 4u * h * HALF;
     float dor[HALF];
     buffer_load_span<VEC>(dor, ubuf, qvalid ? qoff : kNoRow);
+    // The query row and its statistics are requested before delta needs dO·O, so both round trips overlap.
+    constexpr bool NEEDS_Q = MODE == kDqAndDelta || MODE == kDqFromDelta;
+    const Buffer qbuf = make_buffer(sequence(q, w.b, w.head), sequence_bytes(s.queries, q.st, D));
+    float qr[HALF];
+    float m = -INFINITY, l = 0.0f;
+    if constexpr (NEEDS_Q) {
+        buffer_load_span<VEC>(qr, qbuf, qvalid ? static_cast<uint32_t>(query) * (4u * q.st) + 4u * h * HALF : kNoRow);
+        if (qvalid) {
+            m = lse[2 * row];
+            l = lse[2 * row + 1];
+        }
+    }
 
     float dlt;
     if constexpr (MODE == kDqFromDelta) {
@@ -88,25 +128,12 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
         if constexpr (MODE == kDeltaOnly) return;
     }
 
-    const Buffer qbuf = make_buffer(sequence(q, w.b, w.head), sequence_bytes(s.queries, q.st, D));
-    float qr[HALF];
-    buffer_load_span<VEC>(qr, qbuf, qvalid ? static_cast<uint32_t>(query) * (4u * q.st) + 4u * h * HALF : kNoRow);
-    const float m = qvalid ? lse[2 * row] : -INFINITY;
-    const float l = qvalid ? lse[2 * row + 1] : 0.0f;
     // P = exp(s - m) / l = exp2(s·c2 - (m·log2e + log2 l)): the normaliser folds into the exponent offset.
     // A row without visible keys gets offset +inf, so exp2(x - inf) = 0.
     const float mc = m != -INFINITY ? fmaf(m, kLog2e, __log2f(l)) : INFINITY;
 
-    int first, last;
-    const int ntiles = w.valid ? forward_key_range(s, qt, first, last) : 0;
     const int wlo = window_lo(s, query);
     const int whi = window_hi(s, query);
-
-    const Buffer kbuf = make_buffer(sequence(k, w.b, w.head), sequence_bytes(s.keys, k.st, D));
-    const Buffer vbuf = make_buffer(sequence(v, w.b, w.head), sequence_bytes(s.keys, v.st, D));
-    const Buffer mbuf = make_buffer(mask + static_cast<int64_t>(w.b) * s.keys, static_cast<uint32_t>(s.keys));
-    const uint32_t kstep = 4u * k.st;
-    const uint32_t vstep = 4u * v.st;
 
     f32x16 acc[DT];
 #pragma unroll
@@ -173,18 +200,92 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
         }
     };
 
-    // Tiles lead, lead + SPLIT, ...; the count is rounded up to even so the loop body is two straight-line steps.
-    const int mine = ntiles > w.lead ? (ntiles - w.lead + SPLIT - 1) / SPLIT : 0;
-    float ka[HALF], va[HALF], kb[HALF], vb[HALF];
-    int ma = 0, mb = 0;
-    if (mine > 0) load_rows(ka, va, ma, first + w.lead * kTile);
-    for (int i = 0; i < mine; i += 2) {
-        const int key0 = first + (w.lead + i * SPLIT) * kTile;
-        step(ka, va, ma, key0, kb, vb, mb, key0 + SPLIT * kTile);
-        step(kb, vb, mb, key0 + SPLIT * kTile, ka, va, ma, key0 + 2 * SPLIT * kTile);
-    }
+    constexpr int WG = NI > 0 ? NI * SPLIT : kWaves;
+    if constexpr (STAGE) {
+        __shared__ __align__(16) float slots[WG * 2 * kSlotFloats<D>];
+        float *const kslot = slots + 2 * static_cast<int>(threadIdx.x / kWave) * kSlotFloats<D>;
+        float *const vslot = kslot + kSlotFloats<D>;
+        // One key tile: stage r, then load the next tile into r while this one computes.
+        auto stage_step = [&](Raw &r, const int key0, const int next_key0) __attribute__((always_inline)) {
+            const uint32_t bits = key0 < last ? static_cast<uint32_t>(__ballot(r.mask != 0)) : 0u;
+            if (bits == 0) {
+                load_raw(r, next_key0);
+                return;
+            }
+            write_row_tile<D>(kslot, r.k);
+            write_row_tile<D>(vslot, r.v);
+            wave_lds_sync();
+            load_raw(r, next_key0);
 
-    split_sum<SPLIT, DT, (NI > 0 ? NI * SPLIT : kWaves)>(acc, w.sub);
+            f32x16 sc{}, dp{};
+            {
+                float kr[HALF];
+                read_row_layout<D>(kslot, kr);
+#pragma unroll
+                for (int c = 0; c < HALF; ++c) sc = mfma(kr[c], qr[c], sc);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            {
+                float vr[HALF];
+                read_row_layout<D>(vslot, vr);
+#pragma unroll
+                for (int c = 0; c < HALF; ++c) dp = mfma(vr[c], dor[c], dp);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const float p = exp2_fast(fmaf(sc[j], c2, -mc));
+                sc[j] = p * (dp[j] - dlt);
+            }
+            const bool boundary = bits != 0xffffffffu || !tile_in_window(s, q0, key0);
+            if (boundary) {
+                const uint32_t visible = (bits & bit_range(wlo - key0, whi - key0)) >> (4 * h);
+#pragma unroll
+                for (int j = 0; j < 16; ++j) sc[j] = (visible >> (8 * (j >> 2) + (j & 3))) & 1u ? sc[j] : 0.0f;
+            }
+            // dQᵀ += Kᵀ·dSᵀ with K's column layout, eight rows at a time; masked keys contribute nothing,
+            // whatever K holds there.
+            const uint32_t kept = bits >> (4 * h);
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                __builtin_amdgcn_sched_barrier(0);
+                float c[DT][8];
+                if (half == 0) read_column_layout<D, 0, 8>(kslot, c);
+                else read_column_layout<D, 8, 8>(kslot, c);
+                if (bits != 0xffffffffu) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const int jj = 8 * half + j;
+#pragma unroll
+                        for (int t = 0; t < DT; ++t) c[t][j] = (kept >> (8 * (jj >> 2) + (jj & 3))) & 1u ? c[t][j] : 0.0f;
+                    }
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+#pragma unroll
+                    for (int t = 0; t < DT; ++t) acc[t] = mfma(c[t][j], sc[8 * half + j], acc[t]);
+                }
+            }
+        };
+        for (int i = 0; i < mine; ++i) {
+            const int key0 = first + (w.lead + i * SPLIT) * kTile;
+            stage_step(raw, key0, key0 + SPLIT * kTile);
+        }
+        // The slots are free once every wave has left its loop (split_sum_into's first barrier).
+        static_assert(WG * 16 * DT * kWave <= WG * 2 * kSlotFloats<D>);
+        split_sum_into<SPLIT, DT, WG>(acc, w.sub, slots);
+    } else {
+        // Tiles lead, lead + SPLIT, ...; the count is rounded up to even so the loop body is two straight-line steps.
+        float ka[HALF], va[HALF], kb[HALF], vb[HALF];
+        int ma = 0, mb = 0;
+        if (mine > 0) load_rows(ka, va, ma, first + w.lead * kTile);
+        for (int i = 0; i < mine; i += 2) {
+            const int key0 = first + (w.lead + i * SPLIT) * kTile;
+            step(ka, va, ma, key0, kb, vb, mb, key0 + SPLIT * kTile);
+            step(kb, vb, mb, key0 + SPLIT * kTile, ka, va, ma, key0 + 2 * SPLIT * kTile);
+        }
+        split_sum<SPLIT, DT, WG>(acc, w.sub);
+    }
     if (w.sub != 0 || !qvalid) return;
     float *dst = dq + row * D;
 #pragma unroll
@@ -247,6 +348,24 @@ __device__ __forceinline__ void dkdv_tiles(const Tensor &q, const Tensor &k, con
     const Buffer dbuf = make_buffer(delta + static_cast<int64_t>(seq) * s.queries, static_cast<uint32_t>(s.queries) * 4u);
     const uint32_t qstep = 4u * q.st;
     const uint32_t ustep = 4u * du.st;
+
+    // Staged path: raw Q rows and softmax statistics of one query tile, one tile ahead. The first tile's loads go
+    // out before the key tile's mask is known (a fully masked tile ignores them), so they overlap the K/V loads.
+    struct Raw {
+        RowTile<D> q;
+        float m, l, d;
+    };
+    auto load_raw = [&](Raw &r, const int q0) __attribute__((always_inline)) {
+        load_row_tile<D>(r.q, qbuf, qstep, static_cast<uint32_t>(q0) * qstep);
+        const uint32_t qq = static_cast<uint32_t>(q0 + col);
+        r.m = buffer_load(lbuf, qq * 8u, 0);
+        r.l = buffer_load(lbuf, qq * 8u + 4u, 0);
+        r.d = buffer_load(dbuf, qq * 4u, 0);
+    };
+    Raw raw;
+    if constexpr (STAGE) {
+        if (range > start && limit > 0) load_raw(raw, first + start * kTile);
+    }
 
     __shared__ __align__(16) float stats[WAVES][2][kTile];
 
@@ -398,18 +517,6 @@ __device__ __forceinline__ void dkdv_tiles(const Tensor &q, const Tensor &k, con
         static_assert(VEC, "staged tiles need 128-bit access");
         float *const qslot = dkdv_slots<D, WAVES>() + 2 * wave * kSlotFloats<D>;
         float *const uslot = qslot + kSlotFloats<D>;
-        // Raw Q and dO rows and the softmax statistics of one query tile, loaded a tile ahead.
-        struct Raw {
-            RowTile<D> q;
-            float m, l, d;
-        };
-        auto load_raw = [&](Raw &r, const int q0) __attribute__((always_inline)) {
-            load_row_tile<D>(r.q, qbuf, qstep, static_cast<uint32_t>(q0) * qstep);
-            const uint32_t qq = static_cast<uint32_t>(q0 + col);
-            r.m = buffer_load(lbuf, qq * 8u, 0);
-            r.l = buffer_load(lbuf, qq * 8u + 4u, 0);
-            r.d = buffer_load(dbuf, qq * 4u, 0);
-        };
         // One query tile: stage r, then load the next tile's rows into r while this one computes.
         auto stage_step = [&](Raw &r, const int q0, const int next_q0) __attribute__((always_inline)) {
             wave_lds_sync();
@@ -493,11 +600,9 @@ __device__ __forceinline__ void dkdv_tiles(const Tensor &q, const Tensor &k, con
             column_product(uslot, sc, acc_v);
             column_product(qslot, dp, acc_k);
         };
-        Raw r;
-        if (mine > 0) load_raw(r, first + start * kTile);
         for (int i = 0; i < mine; ++i) {
             const int q0 = first + (start + i * stride) * kTile;
-            stage_step(r, q0, q0 + stride * kTile);
+            stage_step(raw, q0, q0 + stride * kTile);
         }
     } else {
         // Tiles start, start + stride, ...; the count is rounded up to even so the loop body is two straight-line
