@@ -190,7 +190,7 @@ def forward_kernel_name(cfg, cus):
         bins = min(items, cus)
         rounds = -(-items // bins)
         return f"rk::attention_forward_kernel<{cfg['width']}, false, true, 4, {3 if rounds == 3 else 2}>"
-    split = 1 if items >= 4096 else 4
+    split = 1 if items >= 8192 else 2 if items >= 4096 else 4  # forward_split_for (attention_launch.hpp)
     return f"rk::attention_forward_kernel<{cfg['width']}, false, true, {split}, 0>"
 
 

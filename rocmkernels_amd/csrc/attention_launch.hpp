@@ -43,11 +43,12 @@ inline bool sequence_fits(const int rows, const rocmkernels_strides &s, const in
     return s.token >= 0 && extent * 4 < (1ll << 31);
 }
 
-// Waves per 32-row work item (see WorkItem in attention_device.hpp): split the streamed dimension over 4 waves
+// Waves per 32-row work item (see WorkItem in attention_device.hpp): split the streamed dimension over several waves
 // when there are too few items to give every SIMD of the MI355X (1024) several waves of its own, not at all for
-// large grids. Measured on MI355X: the forward prefers 4 down to 2048 items; the backward kernels, which hold
-// twice the accumulators and merge them through LDS, prefer 2 there.
-inline int forward_split_for(const long long items) { return items >= 4096 ? 1 : 4; }
+// large grids. Measured on MI355X for the forward: 4 waves per item below 4096 items; 2 from 4096 to 8191 (3-6.5%
+// faster than 1 there, e.g. config 5, 4096 items at d=64: 105.6 -> 98.7 us); 1 from 8192 (2 is 3-5% slower there).
+// The backward kernels, which hold twice the accumulators and merge them through LDS, prefer 2 from 2048 items.
+inline int forward_split_for(const long long items) { return items >= 8192 ? 1 : items >= 4096 ? 2 : 4; }
 inline int backward_split_for(const long long items) { return items >= 4096 ? 1 : items >= 2048 ? 2 : 4; }
 
 // Compute units of the current device (256 on MI355X).
