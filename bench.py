@@ -14,6 +14,10 @@ FLOP accounting:
 Timing: W warm-up launches, then K launches captured in one HIP graph and replayed once between two HIP events on
 the launch stream (device synchronisation on both sides), so host launch gaps do not count; the same K launches
 issued eagerly from Python through ctypes are timed too (``ms_per_launch_eager``). Inputs are resident in HBM.
+Before each timed region the same launches run untimed for at least ``--settle-seconds`` of continuous load: under
+sustained work the MI355X shader clock rises from about 2.0 GHz to about 2.34 GHz within the first ~20 ms (measured
+with s_memtime against s_memrealtime inside the forward kernel; cycles per tile are unchanged), so without it the
+first timed launches would run at the lower clock. The timed launches do the full work of every step.
 """
 import argparse
 import json
@@ -76,11 +80,27 @@ def make_inputs(cfg, device):
     return q, k, v, du, mask, lengths
 
 
+SETTLE_SECONDS = 0.25
+
+
+def settle(launch, per_check=20):
+    """Untimed launches for at least SETTLE_SECONDS of continuous load (`per_check` launches between two looks at
+    the clock), so that the timed launches run at the sustained shader clock rather than the one of an idle GPU."""
+    import torch
+
+    begin = time.perf_counter()
+    while time.perf_counter() - begin < SETTLE_SECONDS:
+        for _ in range(per_check):
+            launch()
+        torch.cuda.synchronize()
+
+
 def time_eager(launch, steps, warmup, stream):
     import torch
 
     for _ in range(warmup):
         launch()
+    settle(launch)
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
@@ -106,6 +126,7 @@ def time_graph(launch, steps, results, exact=True):
     stream = torch.cuda.current_stream()
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
+    settle(graph.replay, per_check=1)
     times = []
     for _ in range(3):
         for r in results:
@@ -260,12 +281,15 @@ def rounded(d):
 
 
 def main():
+    global SETTLE_SECONDS
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=400)
     parser.add_argument("--warmup", type=int, default=40)
     parser.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
     parser.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length (0 skips it)")
+    parser.add_argument("--settle-seconds", type=float, default=SETTLE_SECONDS,
+                        help="untimed continuous load before each timed region (sustained shader clock)")
     parser.add_argument("--no-backward", action="store_true")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
                         help="first copy a buffer of this many MiB on the device (reference for rocprofv3 byte counters)")
@@ -285,6 +309,7 @@ def main():
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    SETTLE_SECONDS = args.settle_seconds
     cfg = CONFIGS[args.config]
     measured = measure(cfg, args.steps, args.warmup, backward=not args.no_backward)
     fwd = measured["forward"]

@@ -1,0 +1,45 @@
+"""bench.py bookkeeping on the CPU: the one-GPU contract, visited-pair counts against closed forms, and the name of the
+forward kernel instance whose launch the roofline object describes."""
+import os
+import subprocess
+import sys
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, ROOT)
+
+import bench  # noqa: E402
+
+
+def test_more_than_one_gpu_is_refused():
+    run = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                         timeout=120)
+    assert run.returncode == 2
+    assert "one GPU" in run.stderr
+
+
+def test_visited_pairs_closed_forms():
+    # Causal without padding: L(L+1)/2 pairs per sequence (config 2: 24 x 524800).
+    cfg = bench.CONFIGS[2]
+    assert bench.visited_pairs(cfg, bench.key_lengths(cfg)) == 24 * 1024 * 1025 // 2
+    # Radius 256 inside the causal band: query q sees min(q, 256) + 1 keys (config 5: 2,072,448 per sequence).
+    cfg = bench.CONFIGS[5]
+    per_sequence = sum(min(q, 256) + 1 for q in range(8192))
+    assert per_sequence == 2072448
+    assert bench.visited_pairs(cfg, bench.key_lengths(cfg)) == 16 * per_sequence
+    # Key padding: query q sees min(q, valid - 1) + 1 keys.
+    cfg = bench.CONFIGS[4]
+    lengths = bench.key_lengths(cfg)
+    assert np.all((lengths >= 1024) & (lengths <= 2048))
+    want = sum(int(np.minimum(np.arange(2048), valid - 1).sum()) + 2048 for valid in lengths)
+    assert bench.visited_pairs(cfg, lengths) == want
+
+
+def test_forward_kernel_names_follow_the_launch_policy():
+    # 256 CUs: config 2 has 768 query tiles (3 per CU, persistent); configs 4 and 5 have 2048 and 4096 (dispatch
+    # order with 4 and 2 waves per tile).
+    assert bench.forward_kernel_name(bench.CONFIGS[2], 256) == "rk::attention_forward_kernel<32, false, true, 4, 3>"
+    assert bench.forward_kernel_name(bench.CONFIGS[1], 256) == "rk::attention_forward_kernel<32, false, true, 4, 0>"
+    assert bench.forward_kernel_name(bench.CONFIGS[4], 256) == "rk::attention_forward_kernel<64, false, true, 4, 0>"
+    assert bench.forward_kernel_name(bench.CONFIGS[5], 256) == "rk::attention_forward_kernel<64, false, true, 2, 0>"
