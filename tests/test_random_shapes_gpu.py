@@ -1,0 +1,96 @@
+"""Seeded random cases through the C ABI against the CPU oracle: head widths 32 and 64 (and 16, 32, 64 in the generic
+forward), lengths around the 32-row tile edges and up to 400, Lq != Lk, radius and causal windows, key padding that
+can empty a batch, token-major and unaligned views (the 32-bit load path), every reference entry point, the default and
+the fused backward. Each case's parameters come from its seed alone (the data from the portable generator), and the
+label of a failure names them."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from parity import check_backward, check_forward, host, normal_case
+from rocmkernels_amd import attention
+
+pytestmark = pytest.mark.gpu
+
+CASES = 48
+GENERIC_CASES = 24
+
+
+def draw(seed, widths):
+    rng = np.random.default_rng(1000 + seed)
+    queries = int(rng.choice([1, 31, 32, 33, 64, int(rng.integers(1, 401))]))
+    keys = queries if rng.random() < 0.5 else int(rng.integers(1, 401))
+    return dict(
+        width=int(rng.choice(widths)),
+        batch=int(rng.integers(1, 4)),
+        heads=int(rng.integers(1, 4)),
+        queries=queries,
+        keys=keys,
+        causal=bool(rng.random() < 0.5),
+        radius=-1 if rng.random() < 0.5 else int(rng.integers(0, 80)),
+        lengths=[int(x) for x in rng.integers(0, keys + 1, size=3)] if rng.random() < 0.5 else None,
+        layout=str(rng.choice(["packed", "token_major", "unaligned"])),
+        entry=str(rng.choice(["simple", "tiled", "flash"])),
+        fused=bool(rng.random() < 0.4),
+    )
+
+
+def key_mask(case):
+    mask = np.ones((case["batch"], case["keys"]), np.uint8)
+    if case["lengths"] is not None:
+        for b in range(case["batch"]):
+            mask[b, case["lengths"][b]:] = 0
+    return mask
+
+
+def place(device, array, layout):
+    """A [B][H][L][D] float32 device view of `array` stored packed, token-major ([B][L][H][D]) or at a 4-byte offset."""
+    if layout == "token_major":
+        return torch.from_numpy(np.ascontiguousarray(array.transpose(0, 2, 1, 3))).to(device).permute(0, 2, 1, 3)
+    if layout == "unaligned":
+        flat = torch.empty(array.size + 1, dtype=torch.float32, device=device)
+        view = flat[1:].view(array.shape)
+        view.copy_(torch.from_numpy(np.ascontiguousarray(array)))
+        return view
+    return torch.from_numpy(np.ascontiguousarray(array)).to(device)
+
+
+def empty_like_layout(device, shape, layout):
+    return place(device, np.zeros(shape, np.float32), layout)
+
+
+@pytest.mark.parametrize("seed", range(CASES))
+def test_random_case_matches_oracle(device, seed):
+    case = draw(seed, [32, 64])
+    label = f"seed {seed}: {case}"
+    q, k, v, du = normal_case(3000 + 10 * seed, case["width"], case["batch"], case["heads"], case["queries"], case["keys"])
+    mask = key_mask(case)
+    want = oracle.attention(q, k, v, mask, du, radius=case["radius"], causal=case["causal"])
+    tq, tk, tv, tdu = (place(device, a, case["layout"]) for a in (q, k, v, du))
+    tm = torch.from_numpy(mask).to(device)
+    out = empty_like_layout(device, q.shape, case["layout"])
+    # Causal runs through the *_ex entry points; otherwise the drawn reference entry point (32-wide) is used.
+    out, lse = attention.forward(tq, tk, tv, tm, radius=case["radius"], causal=case["causal"], output=out,
+                                 entry=case["entry"])
+    backward_entry = "tiled" if case["entry"] == "tiled" else "simple"
+    gq, gk, gv, delta = attention.backward(tq, tk, tv, tm, out, lse, tdu, radius=case["radius"], causal=case["causal"],
+                                           entry=backward_entry, fused=case["fused"])
+    out, lse, gq, gk, gv, delta = host(out, lse, gq, gk, gv, delta)
+    check_forward(out, lse, want, label)
+    check_backward(gq, gk, gv, delta, want, label)
+
+
+@pytest.mark.parametrize("seed", range(GENERIC_CASES))
+def test_random_generic_fp32_case_matches_oracle(device, seed):
+    case = draw(seed + CASES, [16, 32, 64])
+    label = f"seed {seed}: {case}"
+    q, k, v, _ = normal_case(5000 + 10 * seed, case["width"], case["batch"], case["heads"], case["queries"], case["keys"])
+    mask = key_mask(case)
+    want = oracle.attention(q, k, v, mask, radius=case["radius"], causal=False)
+    tq, tk, tv = (place(device, a, case["layout"]) for a in (q, k, v))
+    tm = torch.from_numpy(mask).to(device)
+    out = empty_like_layout(device, q.shape, case["layout"])
+    out, lse = attention.generic_forward(tq, tk, tv, tm, radius=case["radius"], output=out)
+    out, lse = host(out, lse)
+    check_forward(out, lse, want, label)
