@@ -754,6 +754,12 @@ template<int D, bool VEC>
 hipError_t run(const BackwardStage stage, const BackwardArgs &a, const int cus, hipStream_t stream) {
     const int64_t kitems = static_cast<int64_t>((a.keys + kTile - 1) / kTile) * a.batch * a.heads;
     if (stage == kBackwardFused) {
+        // Key-block kernel (one dQ add per element per 128 keys) unless a radius window is set: a block then streams
+        // the union of its four key tiles' windows, three tiles longer than each tile's own (about 25% idle wave-steps
+        // at radius 256), and the per-tile kernel below measured faster (config 5: 305 against 331 us).
+        if constexpr (VEC) {
+            if (a.radius < 0) return launch_fused_backward(D, a, cus, stream);
+        }
         launch_dq<D, kDeltaZeroDq, VEC, 1>(a, stream);
         const hipError_t error = hipGetLastError();
         if (error != hipSuccess) return error;

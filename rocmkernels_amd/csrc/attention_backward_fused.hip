@@ -1,0 +1,529 @@
+// Fused FP32 attention backward for gfx950 (MI355X): one kernel computes dK, dV and dQ, head width 32 or 64, for
+// inputs with 128-bit access (16-byte aligned, strides multiples of 4 floats). Selected by the fused flag of the _ex
+// backward entry points (ROCMKERNELS_ATTENTION_FUSED_BACKWARD); the maths is the reference's backward
+// (Attention.hip:32-169, Attention64.hip:34-191): P = exp(s - max)/sum from the forward's lse, δ = Σ dO·O,
+// dS = P(dO·v - δ), dQ = Σ_k dS·k/√D, dK = Σ_q dS·q/√D, dV = Σ_q P·dO.
+//
+// Mapping. A workgroup owns a key block: 128 keys (four 32-key tiles) of one (batch, head) sequence, and streams the
+// query tiles that see it. Wave w of each query stream owns key tile w of the block (its K and V rows stay in
+// registers, its dKᵀ and dVᵀ accumulate in registers); at d = 32 two streams (8 waves, two per SIMD) take alternate
+// query tiles and merge their dK/dV through LDS at the end, at d = 64 one stream (4 waves, up to 512 registers each).
+// Per query tile, the four waves of a stream share the tile's Q, dO and softmax statistics, staged once in LDS
+// (each wave loads a quarter, whole 128-byte lines, one tile ahead, double-buffered), and each computes
+//   S = Q·Kᵀ and dP = dO·Vᵀ (v_mfma_f32_32x32x2f32, keys on lanes), P and dS = P(dP - δ),
+//   dVᵀ += dOᵀ·P and dKᵀ += Qᵀ·dS (the accumulators of S and dP are the B operands directly),
+// and writes its 32 x 32 dS into the stream's dS tile [query][block key] in LDS. After one workgroup barrier every
+// wave forms one 16-query x 16-feature quadrant of dQ = dS·K/√D over all 128 keys of the block
+// (v_mfma_f32_16x16x4f32: A = dS from LDS, B = the block's K rows held in registers, pre-scaled and zero for masked
+// keys) and adds it into dQ with FP32 buffer atomics: one add per dQ element per key block, a quarter of what adding
+// each 32-key tile's product would take. Per tile and wave that is 5 GEMM tiles of MFMA work, the minimum for the
+// backward (S is recomputed once).
+//
+// Work partition (attention_block_plan.hpp): with a plan, a persistent grid of one workgroup per CU takes
+// cost-balanced pieces (blocks, or contiguous query-tile ranges of blocks too large for one workgroup's share); a piece
+// of a split block adds its dK/dV into memory zeroed by the pre-pass, a whole block stores them. Without a plan (too
+// many pieces for the kernel-argument table), one workgroup per whole block, heaviest first, in dispatch order.
+//
+// A pre-pass kernel computes δ (bit-identical to the deterministic backward's: two half-row FMA chains, then their
+// sum) and zeroes dQ (and dK/dV when some block is split). dQ (and the dK/dV of split blocks) depend on the order in
+// which the atomics land, so their low bits vary from run to run.
+#include "attention_block_plan.hpp"
+#include "attention_device.hpp"
+#include "attention_launch.hpp"
+
+namespace rk {
+
+namespace {
+
+__device__ __forceinline__ f32x4 mfma16(const float a, const float b, const f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+constexpr int kDsStride = kBlockKeys + 4; // floats between dS rows in LDS: conflict-free 128-bit reads of 16 rows
+
+// Feature-major copies of the Q and dO tiles ([feature][query], rows kTStride floats apart) give the column layouts of
+// the dKᵀ and dVᵀ products four tile rows per 128-bit read: accumulator rows tile_row(4u .. 4u + 3, h) are 8u + 4h + 0..3.
+constexpr int kTStride = kTile + 4;
+
+template<int D, int STREAMS>
+struct FusedShared {
+    float qs[STREAMS][2][kSlotFloats<D>]; // Q tile per stream and parity (rows D + 4 floats apart)
+    float us[STREAMS][2][kSlotFloats<D>]; // dO tile
+    float qt[STREAMS][2][D * kTStride];   // Q tile, feature-major
+    float ut[STREAMS][2][D * kTStride];   // dO tile, feature-major
+    float mc[STREAMS][2][kTile];          // per query: exp2 offset m·log2e + log2 l (+inf: P = 0)
+    float dl[STREAMS][2][kTile];          // per query: δ
+    float ds[STREAMS][2][kTile * kDsStride]; // dS[query][block key]
+    uint32_t kbits[kBlockTiles];          // key-mask ballots of the block's key tiles
+};
+
+template<int N>
+struct PieceList {
+    uint32_t entry[N];
+};
+
+// Quarter of a query tile (rows 8w .. 8w + 7) and the statistics of those rows, carried one tile ahead.
+template<int D>
+struct Quarter {
+    f32x4 q[D / 32], u[D / 32];
+    float m, l, d;
+};
+
+template<int D, int STREAMS, bool PLANNED>
+__global__ __launch_bounds__(kWave * kBlockTiles * STREAMS) void attention_fused_backward_kernel(const Tensor q, const Tensor k,
+        const Tensor v, const uint8_t *__restrict__ mask, const float *__restrict__ lse, const Tensor du,
+        const float *__restrict__ delta, float *__restrict__ dq, float *__restrict__ dk, float *__restrict__ dv, const Shape s,
+        const int nblocks, const int slots, const PieceList<PLANNED ? kMaxPieces : 1> table, const float scale) {
+    constexpr int HALF = D / 2;
+    constexpr int DT = D / 32;
+    constexpr int CPR = D / 4; // 16-byte chunks per row
+    __shared__ __align__(16) FusedShared<D, STREAMS> sh;
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int stream = wave / kBlockTiles;
+    const int w = wave - stream * kBlockTiles; // key tile of the block; waves w of both streams share a SIMD
+    const int col = lane & 31;
+    const int h = lane >> 5;
+    const float c2 = scale * kLog2e;
+    // dQ quadrants of this wave: features 16·fg .. +15 of rows 16·rh .. +15 (d = 32: one; d = 64: both row halves).
+    const int fg = D == 32 ? (w & 1) : w;
+    constexpr int RH = D == 32 ? 1 : 2;
+    const int rh0 = D == 32 ? (w >> 1) : 0;
+
+    const int seqs = s.batch * s.heads;
+    const int npieces = PLANNED ? slots : 1;
+    for (int slot = 0; slot < npieces; ++slot) {
+        Piece pc;
+        if constexpr (PLANNED) {
+            const uint32_t e = table.entry[static_cast<int>(blockIdx.x) * slots + slot];
+            if (e == kNoPiece) break;
+            pc = unpack_piece(e);
+        } else {
+            // Rank-major, sequence-minor: under a causal mask block 0 (the heaviest) of every sequence goes first.
+            const int rank = static_cast<int>(blockIdx.x) / seqs;
+            const int seq = static_cast<int>(blockIdx.x) - rank * seqs;
+            pc = Piece{seq * nblocks + rank, 0, 0, false};
+        }
+        const int seq = pc.block / nblocks;
+        const int kb = pc.block - seq * nblocks;
+        const int b = seq / s.heads;
+        const int head = seq - b * s.heads;
+        int qt_first;
+        const int full = block_query_tiles(s.queries, s.keys, s.radius, s.causal, kb, qt_first);
+        const int count = PLANNED ? pc.count : full;
+        const int qt0 = qt_first + pc.start;
+
+        const int kt = kb * kBlockTiles + w;
+        const int key0 = kt * kTile;
+        const int key = key0 + col;
+        const bool in_range = key < s.keys;
+        const Buffer mbuf = make_buffer(mask + static_cast<int64_t>(b) * s.keys, static_cast<uint32_t>(s.keys));
+        int wfirst, wlast; // queries that see some key of this wave's tile
+        dkdv_query_range(s, kt, wfirst, wlast);
+        const int qlo = window_query_lo(s, key);
+        const int qhi = min(window_query_hi(s, key), s.queries - 1);
+
+        const Buffer kbuf = make_buffer(sequence(k, b, head), sequence_bytes(s.keys, k.st, D));
+        const Buffer vbuf = make_buffer(sequence(v, b, head), sequence_bytes(s.keys, v.st, D));
+        const Buffer qbuf = make_buffer(sequence(q, b, head), sequence_bytes(s.queries, q.st, D));
+        const Buffer ubuf = make_buffer(sequence(du, b, head), sequence_bytes(s.queries, du.st, D));
+        const Buffer lbuf = make_buffer(lse + static_cast<int64_t>(seq) * s.queries * 2, static_cast<uint32_t>(s.queries) * 8u);
+        const Buffer dbuf = make_buffer(delta + static_cast<int64_t>(seq) * s.queries, static_cast<uint32_t>(s.queries) * 4u);
+        const Buffer qgbuf = make_buffer(dq + static_cast<int64_t>(seq) * s.queries * D, static_cast<uint32_t>(s.queries) * (4u * D));
+        const uint32_t kstep = 4u * k.st, vstep = 4u * v.st, qstep = 4u * q.st, ustep = 4u * du.st;
+
+        // Quarter loads of a query tile: chunk i * 64 + lane of rows 8w .. 8w + 7 (whole lines), and the statistics of
+        // query q0 + 8w + lane % 8. Rows past the sequence read 0.
+        auto load_quarter = [&](Quarter<D> &r, const int q0) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < D / 32; ++i) {
+                const int c = i * kWave + lane;
+                const uint32_t row = static_cast<uint32_t>(q0 + 8 * w + c / CPR);
+                r.q[i] = buffer_load4(qbuf, row * qstep + 16u * static_cast<uint32_t>(c % CPR), 0);
+                r.u[i] = buffer_load4(ubuf, row * ustep + 16u * static_cast<uint32_t>(c % CPR), 0);
+            }
+            const uint32_t qq = static_cast<uint32_t>(q0 + 8 * w + (lane & 7));
+            r.m = buffer_load(lbuf, qq * 8u, 0);
+            r.l = buffer_load(lbuf, qq * 8u + 4u, 0);
+            r.d = buffer_load(dbuf, qq * 4u, 0);
+        };
+        auto store_quarter = [&](const Quarter<D> &r, const int q0, const int p) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < D / 32; ++i) {
+                const int c = i * kWave + lane;
+                const int at = (8 * w + c / CPR) * kSlotStride<D> + 4 * (c % CPR);
+                *reinterpret_cast<f32x4 *>(&sh.qs[stream][p][at]) = r.q[i];
+                *reinterpret_cast<f32x4 *>(&sh.us[stream][p][at]) = r.u[i];
+                const int tat = 4 * (c % CPR) * kTStride + 8 * w + c / CPR;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    sh.qt[stream][p][tat + e * kTStride] = r.q[i][e];
+                    sh.ut[stream][p][tat + e * kTStride] = r.u[i][e];
+                }
+            }
+            // Every lane writes the statistics of row 8w + lane % 8 (eight lanes write each value, all equal): the loads
+            // then stay with the tile's loads instead of sinking into a branch behind the wait for the tile.
+            const int qq = q0 + 8 * w + (lane & 7);
+            const bool ok = qq < s.queries && r.m != -INFINITY;
+            sh.mc[stream][p][8 * w + (lane & 7)] = ok ? fmaf(r.m, kLog2e, __log2f(r.l)) : INFINITY; // exp2(s·c2 - this) = P
+            sh.dl[stream][p][8 * w + (lane & 7)] = r.d;
+        };
+
+        // The block's rows: this wave's K and V tile in row layout (B operands of S and dP), and the first query tile of
+        // this stream. The dQ B operands (lane (n, kk) holds K[128 kb + 32 kk + i][16 fg + n], i = 0 .. 31: keys 32 kk + i
+        // of the block) are columns of K: the workgroup loads the block's K rows once, a whole 128-byte line per request,
+        // and stages them feature-major in stream 0's dS memory, from which each lane reads its 32 values 4 per 128-bit
+        // read. (32 single-float loads per lane took about 2 us per piece in the texture addresser.)
+        constexpr int WAVES = kBlockTiles * STREAMS;
+        constexpr int KCH = kBlockKeys * CPR / (kWave * WAVES); // 16-byte chunks of the block's K rows per lane
+        static_assert(D * kDsStride <= 2 * kTile * kDsStride, "K block staging region");
+        f32x4 kraw[KCH];
+#pragma unroll
+        for (int i = 0; i < KCH; ++i) {
+            const int c = i * kWave * WAVES + static_cast<int>(threadIdx.x);
+            kraw[i] = buffer_load4(kbuf, static_cast<uint32_t>(kb * kBlockKeys + c / CPR) * kstep + 16u * static_cast<uint32_t>(c % CPR), 0);
+        }
+        float kr[HALF], vr[HALF];
+        buffer_load_span<true>(kr, kbuf, in_range ? static_cast<uint32_t>(key) * kstep + 4u * h * HALF : kNoRow);
+        buffer_load_span<true>(vr, vbuf, in_range ? static_cast<uint32_t>(key) * vstep + 4u * h * HALF : kNoRow);
+        Quarter<D> first;
+        if (stream < count) load_quarter(first, (qt0 + stream) * kTile);
+        // The key mask is read after every other load of the prologue is issued, so the piece waits for memory once.
+        __builtin_amdgcn_sched_barrier(0);
+        const bool visible = in_range && buffer_load_byte(mbuf, static_cast<uint32_t>(key)) != 0;
+        const uint32_t bits = static_cast<uint32_t>(__ballot(visible));
+        float *const kblock = &sh.ds[0][0][0]; // K block, feature-major: kblock[f * kDsStride + key]
+#pragma unroll
+        for (int i = 0; i < KCH; ++i) {
+            const int c = i * kWave * WAVES + static_cast<int>(threadIdx.x);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) kblock[(4 * (c % CPR) + e) * kDsStride + c / CPR] = kraw[i][e];
+        }
+        if (stream < count) store_quarter(first, (qt0 + stream) * kTile, 0);
+        if (stream == 0 && lane == 0) sh.kbits[w] = bits;
+        __syncthreads();
+        float kq[32];
+        {
+            const uint32_t kk_bits = sh.kbits[lane >> 4];
+            const float *src = kblock + (16 * fg + (lane & 15)) * kDsStride + 32 * (lane >> 4);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const f32x4 x = *reinterpret_cast<const f32x4 *>(src + 4 * u);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) kq[4 * u + e] = (kk_bits >> (4 * u + e)) & 1u ? x[e] * scale : 0.0f; // masked keys: 0
+            }
+        }
+        const uint32_t any = __builtin_amdgcn_readfirstlane(sh.kbits[0] | sh.kbits[1] | sh.kbits[2] | sh.kbits[3]);
+        // Every load of the prologue has landed: without this wait the compiler, merging the loop's entry state, keeps
+        // waiting on the whole vector-memory queue (the next tile's prefetch included) inside every step's S and dP chain.
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads(); // the staged K block is read: its memory holds dS from the first step on
+
+        f32x16 acc_k[DT], acc_v[DT];
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+            acc_k[t] = f32x16{};
+            acc_v[t] = f32x16{};
+        }
+        const int nsteps = any != 0 ? (count + STREAMS - 1) / STREAMS : 0;
+        // dQ of a step's tile is formed in the next step, after the barrier that completes the block's dS (dS is
+        // double-buffered): stream 0 does it before its own tile, stream 1 after, so the two waves that share a SIMD
+        // are in different phases and cover each other's LDS waits.
+        auto dq_quadrants = [&](const int i) __attribute__((always_inline)) {
+            const int t = i * STREAMS + stream;
+            if (i < 0 || t >= count) return;
+            const int q0 = (qt0 + t) * kTile;
+            const float *dsp = sh.ds[stream][i & 1];
+#pragma unroll
+            for (int r = 0; r < RH; ++r) {
+                const int rh = rh0 + r;
+                // Rows 16·rh + lane % 16, keys 32·(lane / 16) + 4u .. +3 of dS per 128-bit read.
+                const float *arow = dsp + (16 * rh + (lane & 15)) * kDsStride + 32 * (lane >> 4);
+                f32x4 a[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) a[u] = *reinterpret_cast<const f32x4 *>(arow + 4 * u);
+                f32x4 acc{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+#pragma unroll
+                    for (int x = 0; x < 4; ++x) acc = mfma16(a[u][x], kq[4 * u + x], acc);
+                }
+                // Register x of lane l: query q0 + 16 rh + 4 (l / 16) + x, feature 16 fg + l % 16. Rows past the last
+                // query fall outside the resource and are dropped.
+                const uint32_t voff = (static_cast<uint32_t>(q0 + 16 * rh + 4 * (lane >> 4)) * D + 16u * fg + (lane & 15)) * 4u;
+#pragma unroll
+                for (int x = 0; x < 4; ++x)
+                    __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(acc[x], qgbuf, static_cast<int>(voff + 4u * D * x), 0, 0);
+            }
+        };
+        for (int i = 0; i <= nsteps; ++i) {
+            const int p = i & 1;
+            const int t = i * STREAMS + stream;
+            const bool has = i < nsteps && t < count;
+            const bool has_next = i < nsteps && t + STREAMS < count;
+            const int q0 = (qt0 + t) * kTile;
+            Quarter<D> next;
+            if (has_next) load_quarter(next, q0 + STREAMS * kTile);
+            if (stream == 0) dq_quadrants(i - 1);
+            float *const dsp = sh.ds[stream][p];
+            if (has) {
+                const bool active = bits != 0 && q0 < wlast && q0 + kTile > wfirst;
+                if (active) {
+                    const float *qslot = sh.qs[stream][p];
+                    const float *uslot = sh.us[stream][p];
+                    f32x16 sc{}, dp{};
+                    {
+                        float qr[HALF];
+                        read_row_layout<D>(qslot, qr);
+#pragma unroll
+                        for (int c = 0; c < HALF; ++c) sc = mfma(qr[c], kr[c], sc);
+                    }
+                    {
+                        float ur[HALF];
+                        read_row_layout<D>(uslot, ur);
+#pragma unroll
+                        for (int c = 0; c < HALF; ++c) dp = mfma(ur[c], vr[c], dp);
+                    }
+                    // Accumulator register j holds query q0 + tile_row(j, h): its constants, four rows at a time.
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const f32x4 mcs = *reinterpret_cast<const f32x4 *>(&sh.mc[stream][p][8 * u + 4 * h]);
+                        const f32x4 dls = *reinterpret_cast<const f32x4 *>(&sh.dl[stream][p][8 * u + 4 * h]);
+#pragma unroll
+                        for (int x = 0; x < 4; ++x) {
+                            const int j = 4 * u + x;
+                            const float pr = exp2_fast(fmaf(sc[j], c2, -mcs[x]));
+                            sc[j] = pr;
+                            dp[j] = pr * (dp[j] - dls[x]);
+                        }
+                    }
+                    if (bits != 0xffffffffu || q0 + kTile > s.queries || !tile_in_window(s, q0, key0)) {
+                        const uint32_t keep = visible ? bit_range(qlo - q0, qhi - q0) >> (4 * h) : 0u;
+#pragma unroll
+                        for (int j = 0; j < 16; ++j) {
+                            const bool ok = (keep >> (8 * (j >> 2) + (j & 3))) & 1u;
+                            sc[j] = ok ? sc[j] : 0.0f;
+                            dp[j] = ok ? dp[j] : 0.0f;
+                        }
+                    }
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) dsp[tile_row(j, h) * kDsStride + 32 * w + col] = dp[j];
+                    // dVᵀ += dOᵀ·P and dKᵀ += Qᵀ·dS: A operand of MFMA j is element [tile_row(j, h)][32t + col] of the
+                    // tile, four consecutive j per 128-bit read of the feature-major copy.
+                    auto column_product = [&](const float *slot_t, const f32x16 &bop, f32x16 (&acc)[DT]) __attribute__((always_inline)) {
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            f32x4 c[DT];
+#pragma unroll
+                            for (int t2 = 0; t2 < DT; ++t2)
+                                c[t2] = *reinterpret_cast<const f32x4 *>(slot_t + (32 * t2 + col) * kTStride + 8 * u + 4 * h);
+#pragma unroll
+                            for (int x = 0; x < 4; ++x) {
+#pragma unroll
+                                for (int t2 = 0; t2 < DT; ++t2) acc[t2] = mfma(c[t2][x], bop[4 * u + x], acc[t2]);
+                            }
+                        }
+                    };
+                    column_product(sh.ut[stream][p], sc, acc_v);
+                    column_product(sh.qt[stream][p], dp, acc_k);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) dsp[tile_row(j, h) * kDsStride + 32 * w + col] = 0.0f;
+                }
+            }
+            if (stream != 0) dq_quadrants(i - 1);
+            if (has_next) store_quarter(next, q0 + STREAMS * kTile, p ^ 1);
+            __syncthreads(); // this step's dS and the next step's tiles are in LDS
+        }
+        __syncthreads(); // every wave is done with the dS tiles: the merge below reuses their memory
+
+        if constexpr (STREAMS == 2) {
+            // Stream 1 hands its partial dKᵀ and dVᵀ to stream 0 through LDS (fixed order: deterministic).
+            float *mine = &sh.ds[1][0][0] + w * (2 * 16 * DT * kWave) + lane;
+            if (stream == 1) {
+#pragma unroll
+                for (int t = 0; t < DT; ++t) {
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) {
+                        mine[(16 * t + j) * kWave] = acc_k[t][j];
+                        mine[(16 * (DT + t) + j) * kWave] = acc_v[t][j];
+                    }
+                }
+            }
+            __syncthreads();
+            if (stream == 0) {
+#pragma unroll
+                for (int t = 0; t < DT; ++t) {
+#pragma unroll
+                    for (int j = 0; j < 16; ++j) {
+                        acc_k[t][j] += mine[(16 * t + j) * kWave];
+                        acc_v[t][j] += mine[(16 * (DT + t) + j) * kWave];
+                    }
+                }
+            }
+        }
+        if (stream == 0) {
+            const int64_t krow = (static_cast<int64_t>(seq) * s.keys + key) * D;
+            if (!pc.partial) {
+                if (in_range) {
+#pragma unroll
+                    for (int t = 0; t < DT; ++t) {
+                        store_tile_row<true>(dk + krow + 32 * t, acc_k[t], scale, h);
+                        store_tile_row<true>(dv + krow + 32 * t, acc_v[t], 1.0f, h);
+                    }
+                }
+            } else {
+                // Part of a split block: add into the zeroed dK/dV. The tile goes through this wave's LDS region
+                // transposed (row = key, D + 1 floats apart) so each atomic instruction covers whole 128-byte lines.
+                static_assert(kBlockTiles * kTile * (D + 1) <= 2 * kTile * kDsStride, "transpose region");
+                float *tr = &sh.ds[0][0][0] + w * (kTile * (D + 1));
+                auto add_tile = [&](const f32x16 (&acc)[DT], float *base, const float factor) __attribute__((always_inline)) {
+                    const Buffer gbuf = make_buffer(base + static_cast<int64_t>(seq) * s.keys * D, static_cast<uint32_t>(s.keys) * (4u * D));
+                    wave_lds_sync();
+#pragma unroll
+                    for (int t = 0; t < DT; ++t) {
+#pragma unroll
+                        for (int j = 0; j < 16; ++j) tr[col * (D + 1) + 32 * t + tile_row(j, h)] = acc[t][j] * factor;
+                    }
+                    wave_lds_sync();
+#pragma unroll
+                    for (int r = 0; r < kTile * D / kWave; ++r) {
+                        const int e = r * kWave + lane;
+                        const int row = e / D, f = e - row * D;
+                        const uint32_t voff = (static_cast<uint32_t>(key0 + row) * D + static_cast<uint32_t>(f)) * 4u;
+                        __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(tr[row * (D + 1) + f], gbuf, static_cast<int>(voff), 0, 0);
+                    }
+                };
+                if (bits != 0) {
+                    add_tile(acc_k, dk, scale);
+                    add_tile(acc_v, dv, 1.0f);
+                }
+            }
+        }
+        __syncthreads(); // the next piece reuses the LDS tiles
+    }
+}
+
+// δ = Σ dO·O per query row, dQ = 0, and dK = dV = 0 on the key blocks that the plan splits (those that see more than
+// `split_above` query tiles; their pieces add into dK/dV). Two lanes per row: lane h runs the FMA chain over features
+// h·D/2 .. h·D/2 + D/2 - 1 in order, as each half-wave of the deterministic backward does, and the two halves are added,
+// so δ is bit-identical to that path's.
+template<int D>
+__global__ __launch_bounds__(256) void attention_fused_prepass_kernel(const Tensor o, const Tensor du, float *__restrict__ delta,
+        float *__restrict__ dq, float *__restrict__ dk, float *__restrict__ dv, const Shape s, const int64_t qrows,
+        const int64_t krows, const int split_above) {
+    constexpr int HALF = D / 2;
+    const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t r = t >> 1;
+    const int half = static_cast<int>(t & 1);
+    const f32x4 zero{0.0f, 0.0f, 0.0f, 0.0f};
+    float part = 0.0f;
+    if (r < qrows) {
+        const int64_t seq = r / s.queries;
+        const int query = static_cast<int>(r - seq * s.queries);
+        const int b = static_cast<int>(seq / s.heads), head = static_cast<int>(seq - static_cast<int64_t>(b) * s.heads);
+        const float *orow = o.data + static_cast<int64_t>(b) * o.sb + static_cast<int64_t>(head) * o.sh + static_cast<int64_t>(query) * o.st + half * HALF;
+        const float *urow = du.data + static_cast<int64_t>(b) * du.sb + static_cast<int64_t>(head) * du.sh + static_cast<int64_t>(query) * du.st + half * HALF;
+        f32x4 x[HALF / 4], y[HALF / 4];
+#pragma unroll
+        for (int c = 0; c < HALF / 4; ++c) {
+            x[c] = *reinterpret_cast<const f32x4 *>(urow + 4 * c);
+            y[c] = *reinterpret_cast<const f32x4 *>(orow + 4 * c);
+        }
+#pragma unroll
+        for (int c = 0; c < HALF / 4; ++c) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) part = fmaf(x[c][e], y[c][e], part);
+        }
+        float *dst = dq + r * D + half * HALF;
+#pragma unroll
+        for (int c = 0; c < HALF; c += 4) *reinterpret_cast<f32x4 *>(dst + c) = zero;
+    }
+    const float other = __shfl_xor(part, 1);
+    if (r < qrows && half == 0) delta[r] = part + other;
+    if (r < krows) {
+        const int64_t seq = r / s.keys;
+        const int kb = static_cast<int>(r - seq * s.keys) / kBlockKeys;
+        int first;
+        if (block_query_tiles(s.queries, s.keys, s.radius, s.causal, kb, first) > split_above) {
+            float *kdst = dk + r * D + half * HALF;
+            float *vdst = dv + r * D + half * HALF;
+#pragma unroll
+            for (int c = 0; c < HALF; c += 4) {
+                *reinterpret_cast<f32x4 *>(kdst + c) = zero;
+                *reinterpret_cast<f32x4 *>(vdst + c) = zero;
+            }
+        }
+    }
+}
+
+Tensor tensor(const float *p, const rocmkernels_strides &s) { return Tensor{p, s.batch, s.head, s.token}; }
+
+// The launch's piece table, kept per host thread for the last shape and CU count.
+struct CachedPlan {
+    Shape s{};
+    int cus = -1;
+    bool ok = false;
+    BlockPlan plan;
+    PieceList<kMaxPieces> table;
+};
+
+const CachedPlan &cached_plan(const Shape &s, const int cus) {
+    thread_local CachedPlan cache;
+    const bool same = cache.cus == cus && cache.s.batch == s.batch && cache.s.heads == s.heads && cache.s.queries == s.queries &&
+            cache.s.keys == s.keys && cache.s.radius == s.radius && cache.s.causal == s.causal;
+    if (!same) {
+        const int nblocks = (s.keys + kBlockKeys - 1) / kBlockKeys;
+        cache.ok = plan_blocks(static_cast<long long>(s.batch) * s.heads, nblocks, cus, 3, [&](const int kb) {
+            int first;
+            return block_query_tiles(s.queries, s.keys, s.radius, s.causal, kb, first);
+        }, cache.plan, cache.table.entry);
+        cache.s = s;
+        cache.cus = cus;
+    }
+    return cache;
+}
+
+template<int D>
+hipError_t launch(const BackwardArgs &a, const int cus, hipStream_t stream) {
+    constexpr int STREAMS = D == 32 ? 2 : 1;
+    const Shape shape{a.batch, a.heads, a.queries, a.keys, a.radius, a.causal};
+    const float scale = 1.0f / sqrtf(static_cast<float>(D));
+    const int nblocks = (a.keys + kBlockKeys - 1) / kBlockKeys;
+    const long long seqs = static_cast<long long>(a.batch) * a.heads;
+    const CachedPlan &cp = cached_plan(shape, cus);
+    const bool planned = cp.ok;
+
+    const int64_t qrows = seqs * a.queries, krows = seqs * a.keys;
+    const int64_t rows = qrows > krows ? qrows : krows;
+    // Blocks above the plan's piece length are split (no block is without a plan).
+    const int split_above = planned && cp.plan.partial ? cp.plan.chunk : 0x7fffffff;
+    hipLaunchKernelGGL((attention_fused_prepass_kernel<D>), dim3(static_cast<unsigned>((2 * rows + 255) / 256)), dim3(256), 0, stream,
+            tensor(a.output, a.os), tensor(a.upstream, a.us), a.delta, a.gradient_q, a.gradient_k, a.gradient_v, shape, qrows, krows,
+            split_above);
+    hipError_t error = hipGetLastError();
+    if (error != hipSuccess) return error;
+
+    const unsigned threads = kWave * kBlockTiles * STREAMS;
+    if (planned) {
+        hipLaunchKernelGGL((attention_fused_backward_kernel<D, STREAMS, true>), dim3(static_cast<unsigned>(cp.plan.bins)), dim3(threads),
+                0, stream, tensor(a.q, a.qs), tensor(a.k, a.ks), tensor(a.v, a.vs), reinterpret_cast<const uint8_t *>(a.mask), a.lse,
+                tensor(a.upstream, a.us), a.delta, a.gradient_q, a.gradient_k, a.gradient_v, shape, nblocks, cp.plan.slots, cp.table,
+                scale);
+    } else {
+        const PieceList<1> none{};
+        hipLaunchKernelGGL((attention_fused_backward_kernel<D, STREAMS, false>), dim3(static_cast<unsigned>(seqs * nblocks)), dim3(threads),
+                0, stream, tensor(a.q, a.qs), tensor(a.k, a.ks), tensor(a.v, a.vs), reinterpret_cast<const uint8_t *>(a.mask), a.lse,
+                tensor(a.upstream, a.us), a.delta, a.gradient_q, a.gradient_k, a.gradient_v, shape, nblocks, 1, none, scale);
+    }
+    return hipGetLastError();
+}
+
+} // namespace
+
+hipError_t launch_fused_backward(const int D, const BackwardArgs &a, const int cus, hipStream_t stream) {
+    return D == 32 ? launch<32>(a, cus, stream) : launch<64>(a, cus, stream);
+}
+
+} // namespace rk

@@ -91,4 +91,8 @@ enum BackwardStage {
 
 hipError_t launch_backward(int D, BackwardStage stage, const BackwardArgs &a, hipStream_t stream);
 
+// Fused single-kernel backward over key blocks (attention_backward_fused.hip) for D = 32 or 64 with 128-bit access
+// (every pointer 16-byte aligned, every stride a multiple of 4); called by launch_backward for kBackwardFused.
+hipError_t launch_fused_backward(int D, const BackwardArgs &a, int cus, hipStream_t stream);
+
 } // namespace rk
