@@ -133,15 +133,17 @@ __global__ __launch_bounds__(kWave * kBlockTiles * STREAMS) void attention_fused
         const Buffer qgbuf = make_buffer(dq + static_cast<int64_t>(seq) * s.queries * D, static_cast<uint32_t>(s.queries) * (4u * D));
         const uint32_t kstep = 4u * k.st, vstep = 4u * v.st, qstep = 4u * q.st, ustep = 4u * du.st;
 
-        // Quarter loads of a query tile: chunk i * 64 + lane of rows 8w .. 8w + 7 (whole lines), and the statistics of
-        // query q0 + 8w + lane % 8. Rows past the sequence read 0.
+        // Quarter loads of a query tile: rows 8w .. 8w + 7, lane (row lane % 8, 16-byte chunk 8i + lane / 8) for load i, so
+        // each load covers whole 128-byte lines and a half-wave's feature-major writes below spread over 8 rows (2-way
+        // bank conflicts; with lanes along the row instead, 8-way at d = 64). The statistics are those of query
+        // q0 + 8w + lane % 8. Rows past the sequence read 0.
         auto load_quarter = [&](Quarter<D> &r, const int q0) __attribute__((always_inline)) {
 #pragma unroll
             for (int i = 0; i < D / 32; ++i) {
-                const int c = i * kWave + lane;
-                const uint32_t row = static_cast<uint32_t>(q0 + 8 * w + c / CPR);
-                r.q[i] = buffer_load4(qbuf, row * qstep + 16u * static_cast<uint32_t>(c % CPR), 0);
-                r.u[i] = buffer_load4(ubuf, row * ustep + 16u * static_cast<uint32_t>(c % CPR), 0);
+                const uint32_t row = static_cast<uint32_t>(q0 + 8 * w + (lane & 7));
+                const uint32_t chunk = static_cast<uint32_t>(8 * i + (lane >> 3));
+                r.q[i] = buffer_load4(qbuf, row * qstep + 16u * chunk, 0);
+                r.u[i] = buffer_load4(ubuf, row * ustep + 16u * chunk, 0);
             }
             const uint32_t qq = static_cast<uint32_t>(q0 + 8 * w + (lane & 7));
             r.m = buffer_load(lbuf, qq * 8u, 0);
@@ -151,11 +153,11 @@ __global__ __launch_bounds__(kWave * kBlockTiles * STREAMS) void attention_fused
         auto store_quarter = [&](const Quarter<D> &r, const int q0, const int p) __attribute__((always_inline)) {
 #pragma unroll
             for (int i = 0; i < D / 32; ++i) {
-                const int c = i * kWave + lane;
-                const int at = (8 * w + c / CPR) * kSlotStride<D> + 4 * (c % CPR);
+                const int row = 8 * w + (lane & 7), chunk = 8 * i + (lane >> 3);
+                const int at = row * kSlotStride<D> + 4 * chunk;
                 *reinterpret_cast<f32x4 *>(&sh.qs[stream][p][at]) = r.q[i];
                 *reinterpret_cast<f32x4 *>(&sh.us[stream][p][at]) = r.u[i];
-                const int tat = 4 * (c % CPR) * kTStride + 8 * w + c / CPR;
+                const int tat = 4 * chunk * kTStride + row;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     sh.qt[stream][p][tat + e * kTStride] = r.q[i][e];
