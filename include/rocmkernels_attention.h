@@ -23,8 +23,9 @@
  * The *_ex entry points have no counterpart in the reference: they add `int flags` after `radius`, where
  * bit 0 (ROCMKERNELS_ATTENTION_CAUSAL) restricts every query to keys <= query, and, for the backward only,
  * bit 1 (ROCMKERNELS_ATTENTION_FUSED_BACKWARD) selects the fused backward: dQ is accumulated with FP32 atomics
- * inside the dK/dV pass (fewer matrix products, faster), so its low-order bits may differ from run to run;
- * dK, dV and delta stay bit-reproducible. All other bits must be zero (else hipErrorInvalidValue).
+ * in the same kernel as dK/dV (fewer matrix products, faster), and so are dK/dV of the key blocks whose query range
+ * is split over several workgroups, so their low-order bits may differ from run to run; delta stays
+ * bit-reproducible. All other bits must be zero (else hipErrorInvalidValue).
  */
 #ifndef ROCMKERNELS_ATTENTION_H
 #define ROCMKERNELS_ATTENTION_H
