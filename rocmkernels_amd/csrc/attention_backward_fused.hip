@@ -93,116 +93,149 @@ __global__ __launch_bounds__(kWave * kBlockTiles * STREAMS) void attention_fused
 
     const int seqs = s.batch * s.heads;
     const int npieces = PLANNED ? slots : 1;
-    for (int slot = 0; slot < npieces; ++slot) {
-        Piece pc;
+    const uint32_t kstep = 4u * k.st, vstep = 4u * v.st, qstep = 4u * q.st, ustep = 4u * du.st;
+    constexpr int WAVES = kBlockTiles * STREAMS;
+    constexpr int KCH = kBlockKeys * CPR / (kWave * WAVES); // 16-byte chunks of the block's K rows per lane
+
+    // A piece's coordinates, from its table entry (or, without a plan, from the workgroup index: rank-major,
+    // sequence-minor, so under a causal mask block 0, the heaviest, of every sequence goes first).
+    struct Ctx {
+        bool valid, partial;
+        int seq, kb, b, head, count, qt0;
+    };
+    auto decode = [&](const int slot) __attribute__((always_inline)) {
+        Ctx c{};
+        Piece pc{0, 0, 0, false};
+        c.valid = slot < npieces;
         if constexpr (PLANNED) {
-            const uint32_t e = table.entry[static_cast<int>(blockIdx.x) * slots + slot];
-            if (e == kNoPiece) break;
-            pc = unpack_piece(e);
+            const uint32_t e = c.valid ? table.entry[static_cast<int>(blockIdx.x) * slots + slot] : kNoPiece;
+            c.valid = e != kNoPiece;
+            if (c.valid) pc = unpack_piece(e);
         } else {
-            // Rank-major, sequence-minor: under a causal mask block 0 (the heaviest) of every sequence goes first.
             const int rank = static_cast<int>(blockIdx.x) / seqs;
-            const int seq = static_cast<int>(blockIdx.x) - rank * seqs;
-            pc = Piece{seq * nblocks + rank, 0, 0, false};
+            pc = Piece{(static_cast<int>(blockIdx.x) - rank * seqs) * nblocks + rank, 0, 0, false};
         }
-        const int seq = pc.block / nblocks;
-        const int kb = pc.block - seq * nblocks;
-        const int b = seq / s.heads;
-        const int head = seq - b * s.heads;
+        c.partial = pc.partial;
+        c.seq = pc.block / nblocks;
+        c.kb = pc.block - c.seq * nblocks;
+        c.b = c.seq / s.heads;
+        c.head = c.seq - c.b * s.heads;
         int qt_first;
-        const int full = block_query_tiles(s.queries, s.keys, s.radius, s.causal, kb, qt_first);
-        const int count = PLANNED ? pc.count : full;
-        const int qt0 = qt_first + pc.start;
+        const int full = block_query_tiles(s.queries, s.keys, s.radius, s.causal, c.kb, qt_first);
+        c.count = PLANNED ? pc.count : full;
+        c.qt0 = qt_first + pc.start;
+        return c;
+    };
+    // Per-sequence buffer resources of a piece.
+    struct Bufs {
+        Buffer k, v, q, u, l, d, m;
+    };
+    auto buffers = [&](const Ctx &c) __attribute__((always_inline)) {
+        return Bufs{make_buffer(sequence(k, c.b, c.head), sequence_bytes(s.keys, k.st, D)),
+                make_buffer(sequence(v, c.b, c.head), sequence_bytes(s.keys, v.st, D)),
+                make_buffer(sequence(q, c.b, c.head), sequence_bytes(s.queries, q.st, D)),
+                make_buffer(sequence(du, c.b, c.head), sequence_bytes(s.queries, du.st, D)),
+                make_buffer(lse + static_cast<int64_t>(c.seq) * s.queries * 2, static_cast<uint32_t>(s.queries) * 8u),
+                make_buffer(delta + static_cast<int64_t>(c.seq) * s.queries, static_cast<uint32_t>(s.queries) * 4u),
+                make_buffer(mask + static_cast<int64_t>(c.b) * s.keys, static_cast<uint32_t>(s.keys))};
+    };
+
+    // Quarter loads of a query tile: rows 8w .. 8w + 7, lane (row lane % 8, 16-byte chunk 8i + lane / 8) for load i, so
+    // each load covers whole 128-byte lines and a half-wave's feature-major writes below spread over 8 rows (2-way bank
+    // conflicts; with lanes along the row instead, 8-way at d = 64). The statistics are those of query
+    // q0 + 8w + lane % 8. Rows past the sequence read 0.
+    auto load_quarter = [&](Quarter<D> &r, const Bufs &bf, const int q0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < D / 32; ++i) {
+            const uint32_t row = static_cast<uint32_t>(q0 + 8 * w + (lane & 7));
+            const uint32_t chunk = static_cast<uint32_t>(8 * i + (lane >> 3));
+            r.q[i] = buffer_load4(bf.q, row * qstep + 16u * chunk, 0);
+            r.u[i] = buffer_load4(bf.u, row * ustep + 16u * chunk, 0);
+        }
+        const uint32_t qq = static_cast<uint32_t>(q0 + 8 * w + (lane & 7));
+        r.m = buffer_load(bf.l, qq * 8u, 0);
+        r.l = buffer_load(bf.l, qq * 8u + 4u, 0);
+        r.d = buffer_load(bf.d, qq * 4u, 0);
+    };
+    auto store_quarter = [&](const Quarter<D> &r, const int q0, const int p) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < D / 32; ++i) {
+            const int row = 8 * w + (lane & 7), chunk = 8 * i + (lane >> 3);
+            const int at = row * kSlotStride<D> + 4 * chunk;
+            *reinterpret_cast<f32x4 *>(&sh.qs[stream][p][at]) = r.q[i];
+            *reinterpret_cast<f32x4 *>(&sh.us[stream][p][at]) = r.u[i];
+            const int tat = 4 * chunk * kTStride + row;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                sh.qt[stream][p][tat + e * kTStride] = r.q[i][e];
+                sh.ut[stream][p][tat + e * kTStride] = r.u[i][e];
+            }
+        }
+        // Every lane writes the statistics of row 8w + lane % 8 (eight lanes write each value, all equal): the loads then
+        // stay with the tile's loads instead of sinking into a branch behind the wait for the tile.
+        const int qq = q0 + 8 * w + (lane & 7);
+        const bool ok = qq < s.queries && r.m != -INFINITY;
+        sh.mc[stream][p][8 * w + (lane & 7)] = ok ? fmaf(r.m, kLog2e, __log2f(r.l)) : INFINITY; // exp2(s·c2 - this) = P
+        sh.dl[stream][p][8 * w + (lane & 7)] = r.d;
+    };
+
+    // The loads of a piece's prologue: this wave's K and V tile in row layout (B operands of S and dP), the block's K
+    // rows (whole 128-byte lines, staged feature-major in LDS for the dQ B operands: lane (n, kk) holds
+    // K[128 kb + 32 kk + i][16 fg + n], i = 0 .. 31; 32 single-float loads per lane instead took about 2 us per piece in
+    // the texture addresser), the first query tile of this stream and the key mask byte (issued last: the piece then
+    // waits for memory once). For every piece after the first they are issued during the previous piece's last
+    // iteration, so their round trip overlaps its last dQ and its epilogue.
+    struct Loads {
+        f32x4 kraw[KCH];
+        float kr[HALF], vr[HALF];
+        Quarter<D> first;
+        int mbyte;
+    };
+    auto issue = [&](const Ctx &c, Loads &ld) __attribute__((always_inline)) {
+        const Bufs bf = buffers(c);
+        const int key = (c.kb * kBlockTiles + w) * kTile + col;
+        const bool in_range = key < s.keys;
+#pragma unroll
+        for (int i = 0; i < KCH; ++i) {
+            const int ch = i * kWave * WAVES + static_cast<int>(threadIdx.x);
+            ld.kraw[i] = buffer_load4(bf.k, static_cast<uint32_t>(c.kb * kBlockKeys + ch / CPR) * kstep + 16u * static_cast<uint32_t>(ch % CPR), 0);
+        }
+        buffer_load_span<true>(ld.kr, bf.k, in_range ? static_cast<uint32_t>(key) * kstep + 4u * h * HALF : kNoRow);
+        buffer_load_span<true>(ld.vr, bf.v, in_range ? static_cast<uint32_t>(key) * vstep + 4u * h * HALF : kNoRow);
+        if (stream < c.count) load_quarter(ld.first, bf, (c.qt0 + stream) * kTile);
+        __builtin_amdgcn_sched_barrier(0);
+        ld.mbyte = buffer_load_byte(bf.m, in_range ? static_cast<uint32_t>(key) : kNoRow);
+    };
+
+    Ctx cur = decode(0);
+    Loads ld;
+    if (cur.valid) issue(cur, ld);
+    for (int slot = 0; slot < npieces && cur.valid; ++slot) {
+        const Ctx nxt = decode(slot + 1);
+        const int seq = cur.seq, kb = cur.kb, count = cur.count, qt0 = cur.qt0;
+        const Bufs bf = buffers(cur);
+        const Buffer qgbuf = make_buffer(dq + static_cast<int64_t>(seq) * s.queries * D, static_cast<uint32_t>(s.queries) * (4u * D));
 
         const int kt = kb * kBlockTiles + w;
         const int key0 = kt * kTile;
         const int key = key0 + col;
         const bool in_range = key < s.keys;
-        const Buffer mbuf = make_buffer(mask + static_cast<int64_t>(b) * s.keys, static_cast<uint32_t>(s.keys));
         int wfirst, wlast; // queries that see some key of this wave's tile
         dkdv_query_range(s, kt, wfirst, wlast);
         const int qlo = window_query_lo(s, key);
         const int qhi = min(window_query_hi(s, key), s.queries - 1);
 
-        const Buffer kbuf = make_buffer(sequence(k, b, head), sequence_bytes(s.keys, k.st, D));
-        const Buffer vbuf = make_buffer(sequence(v, b, head), sequence_bytes(s.keys, v.st, D));
-        const Buffer qbuf = make_buffer(sequence(q, b, head), sequence_bytes(s.queries, q.st, D));
-        const Buffer ubuf = make_buffer(sequence(du, b, head), sequence_bytes(s.queries, du.st, D));
-        const Buffer lbuf = make_buffer(lse + static_cast<int64_t>(seq) * s.queries * 2, static_cast<uint32_t>(s.queries) * 8u);
-        const Buffer dbuf = make_buffer(delta + static_cast<int64_t>(seq) * s.queries, static_cast<uint32_t>(s.queries) * 4u);
-        const Buffer qgbuf = make_buffer(dq + static_cast<int64_t>(seq) * s.queries * D, static_cast<uint32_t>(s.queries) * (4u * D));
-        const uint32_t kstep = 4u * k.st, vstep = 4u * v.st, qstep = 4u * q.st, ustep = 4u * du.st;
-
-        // Quarter loads of a query tile: rows 8w .. 8w + 7, lane (row lane % 8, 16-byte chunk 8i + lane / 8) for load i, so
-        // each load covers whole 128-byte lines and a half-wave's feature-major writes below spread over 8 rows (2-way
-        // bank conflicts; with lanes along the row instead, 8-way at d = 64). The statistics are those of query
-        // q0 + 8w + lane % 8. Rows past the sequence read 0.
-        auto load_quarter = [&](Quarter<D> &r, const int q0) __attribute__((always_inline)) {
-#pragma unroll
-            for (int i = 0; i < D / 32; ++i) {
-                const uint32_t row = static_cast<uint32_t>(q0 + 8 * w + (lane & 7));
-                const uint32_t chunk = static_cast<uint32_t>(8 * i + (lane >> 3));
-                r.q[i] = buffer_load4(qbuf, row * qstep + 16u * chunk, 0);
-                r.u[i] = buffer_load4(ubuf, row * ustep + 16u * chunk, 0);
-            }
-            const uint32_t qq = static_cast<uint32_t>(q0 + 8 * w + (lane & 7));
-            r.m = buffer_load(lbuf, qq * 8u, 0);
-            r.l = buffer_load(lbuf, qq * 8u + 4u, 0);
-            r.d = buffer_load(dbuf, qq * 4u, 0);
-        };
-        auto store_quarter = [&](const Quarter<D> &r, const int q0, const int p) __attribute__((always_inline)) {
-#pragma unroll
-            for (int i = 0; i < D / 32; ++i) {
-                const int row = 8 * w + (lane & 7), chunk = 8 * i + (lane >> 3);
-                const int at = row * kSlotStride<D> + 4 * chunk;
-                *reinterpret_cast<f32x4 *>(&sh.qs[stream][p][at]) = r.q[i];
-                *reinterpret_cast<f32x4 *>(&sh.us[stream][p][at]) = r.u[i];
-                const int tat = 4 * chunk * kTStride + row;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    sh.qt[stream][p][tat + e * kTStride] = r.q[i][e];
-                    sh.ut[stream][p][tat + e * kTStride] = r.u[i][e];
-                }
-            }
-            // Every lane writes the statistics of row 8w + lane % 8 (eight lanes write each value, all equal): the loads
-            // then stay with the tile's loads instead of sinking into a branch behind the wait for the tile.
-            const int qq = q0 + 8 * w + (lane & 7);
-            const bool ok = qq < s.queries && r.m != -INFINITY;
-            sh.mc[stream][p][8 * w + (lane & 7)] = ok ? fmaf(r.m, kLog2e, __log2f(r.l)) : INFINITY; // exp2(s·c2 - this) = P
-            sh.dl[stream][p][8 * w + (lane & 7)] = r.d;
-        };
-
-        // The block's rows: this wave's K and V tile in row layout (B operands of S and dP), and the first query tile of
-        // this stream. The dQ B operands (lane (n, kk) holds K[128 kb + 32 kk + i][16 fg + n], i = 0 .. 31: keys 32 kk + i
-        // of the block) are columns of K: the workgroup loads the block's K rows once, a whole 128-byte line per request,
-        // and stages them feature-major in stream 0's dS memory, from which each lane reads its 32 values 4 per 128-bit
-        // read. (32 single-float loads per lane took about 2 us per piece in the texture addresser.)
-        constexpr int WAVES = kBlockTiles * STREAMS;
-        constexpr int KCH = kBlockKeys * CPR / (kWave * WAVES); // 16-byte chunks of the block's K rows per lane
-        static_assert(D * kDsStride <= 2 * kTile * kDsStride, "K block staging region");
-        f32x4 kraw[KCH];
-#pragma unroll
-        for (int i = 0; i < KCH; ++i) {
-            const int c = i * kWave * WAVES + static_cast<int>(threadIdx.x);
-            kraw[i] = buffer_load4(kbuf, static_cast<uint32_t>(kb * kBlockKeys + c / CPR) * kstep + 16u * static_cast<uint32_t>(c % CPR), 0);
-        }
-        float kr[HALF], vr[HALF];
-        buffer_load_span<true>(kr, kbuf, in_range ? static_cast<uint32_t>(key) * kstep + 4u * h * HALF : kNoRow);
-        buffer_load_span<true>(vr, vbuf, in_range ? static_cast<uint32_t>(key) * vstep + 4u * h * HALF : kNoRow);
-        Quarter<D> first;
-        if (stream < count) load_quarter(first, (qt0 + stream) * kTile);
-        // The key mask is read after every other load of the prologue is issued, so the piece waits for memory once.
-        __builtin_amdgcn_sched_barrier(0);
-        const bool visible = in_range && buffer_load_byte(mbuf, static_cast<uint32_t>(key)) != 0;
+        const bool visible = in_range && ld.mbyte != 0;
         const uint32_t bits = static_cast<uint32_t>(__ballot(visible));
+        static_assert(D * kDsStride <= 2 * kTile * kDsStride, "K block staging region");
         float *const kblock = &sh.ds[0][0][0]; // K block, feature-major: kblock[f * kDsStride + key]
 #pragma unroll
         for (int i = 0; i < KCH; ++i) {
-            const int c = i * kWave * WAVES + static_cast<int>(threadIdx.x);
+            const int ch = i * kWave * WAVES + static_cast<int>(threadIdx.x);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) kblock[(4 * (c % CPR) + e) * kDsStride + c / CPR] = kraw[i][e];
+            for (int e = 0; e < 4; ++e) kblock[(4 * (ch % CPR) + e) * kDsStride + ch / CPR] = ld.kraw[i][e];
         }
-        if (stream < count) store_quarter(first, (qt0 + stream) * kTile, 0);
+        if (stream < count) store_quarter(ld.first, (qt0 + stream) * kTile, 0);
         if (stream == 0 && lane == 0) sh.kbits[w] = bits;
         __syncthreads();
         float kq[32];
@@ -221,6 +254,8 @@ __global__ __launch_bounds__(kWave * kBlockTiles * STREAMS) void attention_fused
         // waiting on the whole vector-memory queue (the next tile's prefetch included) inside every step's S and dP chain.
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads(); // the staged K block is read: its memory holds dS from the first step on
+        float (&kr)[HALF] = ld.kr;
+        float (&vr)[HALF] = ld.vr;
 
         f32x16 acc_k[DT], acc_v[DT];
 #pragma unroll
@@ -259,14 +294,14 @@ __global__ __launch_bounds__(kWave * kBlockTiles * STREAMS) void attention_fused
                     __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(acc[x], qgbuf, static_cast<int>(voff + 4u * D * x), 0, 0);
             }
         };
-        for (int i = 0; i <= nsteps; ++i) {
+        for (int i = 0; i < nsteps; ++i) {
             const int p = i & 1;
             const int t = i * STREAMS + stream;
-            const bool has = i < nsteps && t < count;
-            const bool has_next = i < nsteps && t + STREAMS < count;
+            const bool has = t < count;
+            const bool has_next = t + STREAMS < count;
             const int q0 = (qt0 + t) * kTile;
             Quarter<D> next;
-            if (has_next) load_quarter(next, q0 + STREAMS * kTile);
+            if (has_next) load_quarter(next, bf, q0 + STREAMS * kTile);
             if (stream == 0) dq_quadrants(i - 1);
             float *const dsp = sh.ds[stream][p];
             if (has) {
@@ -338,6 +373,10 @@ __global__ __launch_bounds__(kWave * kBlockTiles * STREAMS) void attention_fused
             if (has_next) store_quarter(next, q0 + STREAMS * kTile, p ^ 1);
             __syncthreads(); // this step's dS and the next step's tiles are in LDS
         }
+        // dQ of the last tile. This piece's K/V rows are dead: the next piece's loads go out first, and their round trip
+        // overlaps this dQ and the epilogue below.
+        if (nxt.valid) issue(nxt, ld);
+        dq_quadrants(nsteps - 1);
         __syncthreads(); // every wave is done with the dS tiles: the merge below reuses their memory
 
         if constexpr (STREAMS == 2) {
@@ -366,13 +405,23 @@ __global__ __launch_bounds__(kWave * kBlockTiles * STREAMS) void attention_fused
             }
         }
         if (stream == 0) {
-            const int64_t krow = (static_cast<int64_t>(seq) * s.keys + key) * D;
-            if (!pc.partial) {
-                if (in_range) {
+            if (!cur.partial) {
+                // Buffer stores (sequence base in SGPRs, 32-bit offsets; keys past the end fall outside the resource):
+                // 64-bit row pointers here were spilled to scratch, and the reload's wait then also waited for the next
+                // piece's loads, which are in flight by now.
+                const Buffer kg = make_buffer(dk + static_cast<int64_t>(seq) * s.keys * D, static_cast<uint32_t>(s.keys) * (4u * D));
+                const Buffer vg = make_buffer(dv + static_cast<int64_t>(seq) * s.keys * D, static_cast<uint32_t>(s.keys) * (4u * D));
+                const uint32_t row = static_cast<uint32_t>(key) * (4u * D) + 16u * h;
 #pragma unroll
-                    for (int t = 0; t < DT; ++t) {
-                        store_tile_row<true>(dk + krow + 32 * t, acc_k[t], scale, h);
-                        store_tile_row<true>(dv + krow + 32 * t, acc_v[t], 1.0f, h);
+                for (int t = 0; t < DT; ++t) {
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const uint32_t off = row + 128u * t + 32u * u; // features 32t + 8u + 4h .. +3
+                        const f32x4 xk{acc_k[t][4 * u] * scale, acc_k[t][4 * u + 1] * scale, acc_k[t][4 * u + 2] * scale,
+                                acc_k[t][4 * u + 3] * scale};
+                        const f32x4 xv{acc_v[t][4 * u], acc_v[t][4 * u + 1], acc_v[t][4 * u + 2], acc_v[t][4 * u + 3]};
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, xk), kg, static_cast<int>(off), 0, 0);
+                        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, xv), vg, static_cast<int>(off), 0, 0);
                     }
                 }
             } else {
@@ -404,6 +453,7 @@ __global__ __launch_bounds__(kWave * kBlockTiles * STREAMS) void attention_fused
             }
         }
         __syncthreads(); // the next piece reuses the LDS tiles
+        cur = nxt;
     }
 }
 
