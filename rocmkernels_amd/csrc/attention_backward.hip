@@ -66,7 +66,7 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
     // this wave's LDS slots, which give the row layouts (Sᵀ, dPᵀ operands) and K's column layout (dQᵀ operand). The
     // first tile's loads go out before the query row's, so a wave waits for memory once before its first tile
     // (issued after delta, they arrived 3-9 us after launch at the 24 x 1024 causal shape).
-    constexpr bool STAGE = NI > 0 && VEC && (MODE == kDqAndDelta || MODE == kDqFromDelta);
+    constexpr bool STAGE = (NI > 0 || D == 64) && VEC && (MODE == kDqAndDelta || MODE == kDqFromDelta);
     struct Raw {
         RowTile<D> k, v;
         int mask;
@@ -635,10 +635,11 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
     }();
     const int kt = w.valid ? w.rank : ktiles; // past the last key tile: no work
     f32x16 acc_k[DT], acc_v[DT];
-    dkdv_tiles<D, VEC, FUSED, WG, (NI > 0)>(q, k, v, mask, lse, du, delta, dq, s, scale, w.b, w.head, kt, w.lead, SPLIT,
+    constexpr bool STAGE = (NI > 0 || (VEC && D == 64)) && !FUSED;
+    dkdv_tiles<D, VEC, FUSED, WG, STAGE>(q, k, v, mask, lse, du, delta, dq, s, scale, w.b, w.head, kt, w.lead, SPLIT,
             0x7fffffff, acc_k, acc_v);
 
-    if constexpr (NI > 0) { // the staged path's LDS slots are free once every wave has left its loop
+    if constexpr (STAGE) { // the staged path's LDS slots are free once every wave has left its loop
         static_assert(WG * 16 * DT * kWave <= WG * 2 * kSlotFloats<D>);
         split_sum_into<SPLIT, DT, WG>(acc_k, w.sub, dkdv_slots<D, WG>());
         split_sum_into<SPLIT, DT, WG>(acc_v, w.sub, dkdv_slots<D, WG>());
