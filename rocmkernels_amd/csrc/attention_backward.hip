@@ -62,11 +62,13 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
     const uint32_t kstep = 4u * k.st;
     const uint32_t vstep = 4u * v.st;
 
-    // Persistent grid with 128-bit access: each K and V tile is loaded a whole line per request and staged through
-    // this wave's LDS slots, which give the row layouts (Sᵀ, dPᵀ operands) and K's column layout (dQᵀ operand). The
-    // first tile's loads go out before the query row's, so a wave waits for memory once before its first tile
-    // (issued after delta, they arrived 3-9 us after launch at the 24 x 1024 causal shape).
-    constexpr bool STAGE = (NI > 0 || D == 64) && VEC && (MODE == kDqAndDelta || MODE == kDqFromDelta);
+    // With 128-bit access each K and V tile is loaded a whole line per request and staged through this wave's LDS slots,
+    // which give the row layouts (Sᵀ, dPᵀ operands) and K's column layout (dQᵀ operand). The first tile's loads go out
+    // before the query row's, so a wave waits for memory once before its first tile (issued after delta, they arrived
+    // 3-9 us after launch at the 24 x 1024 causal shape). Reading K's columns straight from memory instead took 49
+    // vector-memory loads per tile at d = 64, more than a wave can keep outstanding (63) with the next tile in flight:
+    // staging made the d = 64 backward 9-15% faster (configs 4 and 5) and d = 32 up to 6% on large grids.
+    constexpr bool STAGE = VEC && (MODE == kDqAndDelta || MODE == kDqFromDelta);
     struct Raw {
         RowTile<D> k, v;
         int mask;
@@ -299,7 +301,8 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
 // STAGE (128-bit access only): each Q and dO tile is loaded a whole line per request and staged through this wave's
 // LDS slots, from which the wave reads both the row layout (S and dP operands) and the column layout (dK and dV
 // operands); one register set of raw rows is carried a tile ahead. That needs about 70 fewer registers than the row
-// spans plus column loads (two sets of rows in flight), enough for three waves per SIMD at D = 32.
+// spans plus column loads (two sets of rows in flight), enough for three waves per SIMD at D = 32, and 19 instead of 83
+// vector-memory loads per tile at D = 64 (a wave keeps at most 63 outstanding).
 // LDS slots of the staged dK/dV path: a Q tile and a dO tile per wave.
 template<int D, int WAVES>
 __device__ __forceinline__ float *dkdv_slots() {
@@ -635,7 +638,7 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
     }();
     const int kt = w.valid ? w.rank : ktiles; // past the last key tile: no work
     f32x16 acc_k[DT], acc_v[DT];
-    constexpr bool STAGE = (NI > 0 || (VEC && D == 64)) && !FUSED;
+    constexpr bool STAGE = VEC && !FUSED;
     dkdv_tiles<D, VEC, FUSED, WG, STAGE>(q, k, v, mask, lse, du, delta, dq, s, scale, w.b, w.head, kt, w.lead, SPLIT,
             0x7fffffff, acc_k, acc_v);
 
