@@ -755,20 +755,25 @@ void launch_dkdv_mapped(const BackwardArgs &a, const int cus, hipStream_t stream
 
 
 template<int D, bool VEC>
-hipError_t run(const BackwardStage stage, const BackwardArgs &a, const int cus, hipStream_t stream) {
+hipError_t run(BackwardStage stage, const BackwardArgs &a, const int cus, hipStream_t stream) {
     const int64_t kitems = static_cast<int64_t>((a.keys + kTile - 1) / kTile) * a.batch * a.heads;
     if (stage == kBackwardFused) {
         // Key-block kernel (one dQ add per element per 128 keys) unless a radius window is set: a block then streams
         // the union of its four key tiles' windows, three tiles longer than each tile's own (about 25% idle wave-steps
-        // at radius 256), and the per-tile kernel below measured faster (config 5: 305 against 331 us).
+        // at radius 256). Under a radius window the deterministic kernels, with staged tiles, measured fastest
+        // (config 5: 299 us, against 305 for the per-tile fused kernel and 331 for the key-block kernel), so the flag
+        // runs them: their results are also reproducible, which the flag allows but does not promise.
         if constexpr (VEC) {
             if (a.radius < 0) return launch_fused_backward(D, a, cus, stream);
+            stage = kBackwardAll; // the deterministic kernels below
+        } else {
+            // Without 128-bit access: delta and dQ = 0, then the per-key-tile dK/dV kernel adding dQ per 32 x 32 tile.
+            launch_dq<D, kDeltaZeroDq, VEC, 1>(a, stream);
+            const hipError_t error = hipGetLastError();
+            if (error != hipSuccess) return error;
+            launch_dkdv_split<D, VEC, true>(a, backward_split_for(kitems), stream);
+            return hipGetLastError();
         }
-        launch_dq<D, kDeltaZeroDq, VEC, 1>(a, stream);
-        const hipError_t error = hipGetLastError();
-        if (error != hipSuccess) return error;
-        launch_dkdv_split<D, VEC, true>(a, backward_split_for(kitems), stream);
-        return hipGetLastError();
     }
     if (stage == kBackwardAll || stage == kBackwardDelta || stage == kBackwardQuery) {
         if (stage == kBackwardDelta) launch_dq<D, kDeltaOnly, VEC, 1>(a, stream);
