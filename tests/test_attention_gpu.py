@@ -433,11 +433,11 @@ def test_fused_backward_config3_and_masked_batch(device):
     assert np.array_equal(delta.view(np.int32), ddelta.view(np.int32))
 
 
-@pytest.mark.parametrize("width,batch,length,radius", [(32, 64, 2048, -1), (64, 16, 8192, 256)])
+@pytest.mark.parametrize("width,batch,length,radius", [(32, 64, 2048, -1), (64, 32, 4096, -1), (64, 16, 8192, 256)])
 def test_fused_backward_dispatch_order_subset(device, width, batch, length, radius):
-    # 64 x 2048 causal: more key blocks (1024) than the piece table holds, so one workgroup per whole block in dispatch
-    # order, every dK/dV stored. Config 5 (radius 256) takes the per-key-tile fused kernel. Checked on two sequences
-    # against the oracle, and the whole batch against the deterministic backward.
+    # 64 x 2048 causal at d=32 and 32 x 4096 at d=64: more key blocks (1024) than the piece table holds, so one workgroup
+    # per whole block in dispatch order, every dK/dV stored. Config 5 (radius 256): the fused flag runs the deterministic
+    # kernels. Checked on two sequences against the oracle, and the whole batch against the deterministic backward.
     q, k, v, du = normal_case(960 + width, width, batch, 1, length, length)
     mask = np.ones((batch, length), np.uint8)
     mask[1, length // 3:] = 0
