@@ -51,8 +51,8 @@ struct FusedShared {
     float us[STREAMS][2][kSlotFloats<D>]; // dO tile
     float qt[STREAMS][2][D * kTStride];   // Q tile, feature-major
     float ut[STREAMS][2][D * kTStride];   // dO tile, feature-major
-    float mc[STREAMS][2][kTile];          // per query: exp2 offset m·log2e + log2 l (+inf: P = 0)
-    float dl[STREAMS][2][kTile];          // per query: δ
+    float mc[STREAMS][2][kTile];          // per query: S chain seed -(m·log2e + log2 l) (-inf: P = 0)
+    float dl[STREAMS][2][kTile];          // per query: dP chain seed -δ
     float ds[STREAMS][2][kTile * kDsStride]; // dS[query][block key]
     uint32_t kbits[kBlockTiles];          // key-mask ballots of the block's key tiles
 };
@@ -175,8 +175,8 @@ __global__ __launch_bounds__(kWave * kBlockTiles * STREAMS) void attention_fused
         // stay with the tile's loads instead of sinking into a branch behind the wait for the tile.
         const int qq = q0 + 8 * w + (lane & 7);
         const bool ok = qq < s.queries && r.m != -INFINITY;
-        sh.mc[stream][p][8 * w + (lane & 7)] = ok ? fmaf(r.m, kLog2e, __log2f(r.l)) : INFINITY; // exp2(s·c2 - this) = P
-        sh.dl[stream][p][8 * w + (lane & 7)] = r.d;
+        sh.mc[stream][p][8 * w + (lane & 7)] = ok ? -fmaf(r.m, kLog2e, __log2f(r.l)) : -INFINITY; // P = exp2(s·c2 + this)
+        sh.dl[stream][p][8 * w + (lane & 7)] = -r.d;
     };
 
     // The loads of a piece's prologue: this wave's K and V tile in row layout (B operands of S and dP), the block's K
@@ -256,6 +256,10 @@ __global__ __launch_bounds__(kWave * kBlockTiles * STREAMS) void attention_fused
         __syncthreads(); // the staged K block is read: its memory holds dS from the first step on
         float (&kr)[HALF] = ld.kr;
         float (&vr)[HALF] = ld.vr;
+        // S·scale·log2e comes straight out of the S MFMAs (K pre-scaled here), whose chain starts from the query's
+        // -(m·log2e + log2 l), so P = exp2(chain); the dP chain starts from -δ, so dS = P·chain.
+#pragma unroll
+        for (int c = 0; c < HALF; ++c) kr[c] *= c2;
 
         f32x16 acc_k[DT], acc_v[DT];
 #pragma unroll
@@ -309,7 +313,18 @@ __global__ __launch_bounds__(kWave * kBlockTiles * STREAMS) void attention_fused
                 if (active) {
                     const float *qslot = sh.qs[stream][p];
                     const float *uslot = sh.us[stream][p];
-                    f32x16 sc{}, dp{};
+                    // Accumulator register j holds query q0 + tile_row(j, h): the chains start from its seeds.
+                    f32x16 sc, dp;
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const f32x4 mcs = *reinterpret_cast<const f32x4 *>(&sh.mc[stream][p][8 * u + 4 * h]);
+                        const f32x4 dls = *reinterpret_cast<const f32x4 *>(&sh.dl[stream][p][8 * u + 4 * h]);
+#pragma unroll
+                        for (int x = 0; x < 4; ++x) {
+                            sc[4 * u + x] = mcs[x];
+                            dp[4 * u + x] = dls[x];
+                        }
+                    }
                     {
                         float qr[HALF];
                         read_row_layout<D>(qslot, qr);
@@ -322,18 +337,11 @@ __global__ __launch_bounds__(kWave * kBlockTiles * STREAMS) void attention_fused
 #pragma unroll
                         for (int c = 0; c < HALF; ++c) dp = mfma(ur[c], vr[c], dp);
                     }
-                    // Accumulator register j holds query q0 + tile_row(j, h): its constants, four rows at a time.
 #pragma unroll
-                    for (int u = 0; u < 4; ++u) {
-                        const f32x4 mcs = *reinterpret_cast<const f32x4 *>(&sh.mc[stream][p][8 * u + 4 * h]);
-                        const f32x4 dls = *reinterpret_cast<const f32x4 *>(&sh.dl[stream][p][8 * u + 4 * h]);
-#pragma unroll
-                        for (int x = 0; x < 4; ++x) {
-                            const int j = 4 * u + x;
-                            const float pr = exp2_fast(fmaf(sc[j], c2, -mcs[x]));
-                            sc[j] = pr;
-                            dp[j] = pr * (dp[j] - dls[x]);
-                        }
+                    for (int j = 0; j < 16; ++j) {
+                        const float pr = exp2_fast(sc[j]);
+                        sc[j] = pr;
+                        dp[j] *= pr;
                     }
                     if (bits != 0xffffffffu || q0 + kTile > s.queries || !tile_in_window(s, q0, key0)) {
                         const uint32_t keep = visible ? bit_range(qlo - q0, qhi - q0) >> (4 * h) : 0u;
