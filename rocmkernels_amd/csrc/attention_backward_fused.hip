@@ -466,20 +466,22 @@ __global__ __launch_bounds__(kWave * kBlockTiles * STREAMS) void attention_fused
 }
 
 // δ = Σ dO·O per query row, dQ = 0, and dK = dV = 0 on the key blocks that the plan splits (those that see more than
-// `split_above` query tiles; their pieces add into dK/dV). Two lanes per row: lane h runs the FMA chain over features
-// h·D/2 .. h·D/2 + D/2 - 1 in order, as each half-wave of the deterministic backward does, and the two halves are added,
-// so δ is bit-identical to that path's.
+// `split_above` query tiles; their pieces add into dK/dV). Threads 0 .. 2·qrows - 1 compute δ, two lanes per row: lane h
+// runs the FMA chain over features h·D/2 .. h·D/2 + D/2 - 1 in order, as each half-wave of the deterministic backward
+// does, and the two halves are added, so δ is bit-identical to that path's. Every thread also clears one 16-byte group
+// of a dQ row and of a dK/dV row: D/4 times more waves than one row per lane pair (192 workgroups at 24 x 1024, fewer
+// than the CUs), which keeps enough stores in flight.
 template<int D>
 __global__ __launch_bounds__(256) void attention_fused_prepass_kernel(const Tensor o, const Tensor du, float *__restrict__ delta,
         float *__restrict__ dq, float *__restrict__ dk, float *__restrict__ dv, const Shape s, const int64_t qrows,
         const int64_t krows, const int split_above) {
     constexpr int HALF = D / 2;
+    constexpr int G = D / 4; // 16-byte groups per row
     const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    const int64_t r = t >> 1;
-    const int half = static_cast<int>(t & 1);
     const f32x4 zero{0.0f, 0.0f, 0.0f, 0.0f};
-    float part = 0.0f;
-    if (r < qrows) {
+    if (t < 2 * qrows) { // both lanes of a row pair are inside or outside
+        const int64_t r = t >> 1;
+        const int half = static_cast<int>(t & 1);
         const int64_t seq = r / s.queries;
         const int query = static_cast<int>(r - seq * s.queries);
         const int b = static_cast<int>(seq / s.heads), head = static_cast<int>(seq - static_cast<int64_t>(b) * s.heads);
@@ -491,29 +493,24 @@ __global__ __launch_bounds__(256) void attention_fused_prepass_kernel(const Tens
             x[c] = *reinterpret_cast<const f32x4 *>(urow + 4 * c);
             y[c] = *reinterpret_cast<const f32x4 *>(orow + 4 * c);
         }
+        float part = 0.0f;
 #pragma unroll
         for (int c = 0; c < HALF / 4; ++c) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) part = fmaf(x[c][e], y[c][e], part);
         }
-        float *dst = dq + r * D + half * HALF;
-#pragma unroll
-        for (int c = 0; c < HALF; c += 4) *reinterpret_cast<f32x4 *>(dst + c) = zero;
+        const float other = __shfl_xor(part, 1);
+        if (half == 0) delta[r] = part + other;
     }
-    const float other = __shfl_xor(part, 1);
-    if (r < qrows && half == 0) delta[r] = part + other;
-    if (r < krows) {
-        const int64_t seq = r / s.keys;
-        const int kb = static_cast<int>(r - seq * s.keys) / kBlockKeys;
+    if (t < qrows * G) reinterpret_cast<f32x4 *>(dq)[t] = zero;
+    if (t < krows * G) {
+        const int64_t r = t / G;
+        // Key index within its sequence; 32-bit arithmetic whenever the key rows fit (always, short of 2^32 rows).
+        const int key = static_cast<int>(krows <= 0xffffffffLL ? static_cast<uint32_t>(r) % static_cast<uint32_t>(s.keys) : r % s.keys);
         int first;
-        if (block_query_tiles(s.queries, s.keys, s.radius, s.causal, kb, first) > split_above) {
-            float *kdst = dk + r * D + half * HALF;
-            float *vdst = dv + r * D + half * HALF;
-#pragma unroll
-            for (int c = 0; c < HALF; c += 4) {
-                *reinterpret_cast<f32x4 *>(kdst + c) = zero;
-                *reinterpret_cast<f32x4 *>(vdst + c) = zero;
-            }
+        if (block_query_tiles(s.queries, s.keys, s.radius, s.causal, key / kBlockKeys, first) > split_above) {
+            reinterpret_cast<f32x4 *>(dk)[t] = zero;
+            reinterpret_cast<f32x4 *>(dv)[t] = zero;
         }
     }
 }
@@ -559,7 +556,8 @@ hipError_t launch(const BackwardArgs &a, const int cus, hipStream_t stream) {
     const int64_t rows = qrows > krows ? qrows : krows;
     // Blocks above the plan's piece length are split (no block is without a plan).
     const int split_above = planned && cp.plan.partial ? cp.plan.chunk : 0x7fffffff;
-    hipLaunchKernelGGL((attention_fused_prepass_kernel<D>), dim3(static_cast<unsigned>((2 * rows + 255) / 256)), dim3(256), 0, stream,
+    const int64_t threads_pre = (2 * qrows > rows * (D / 4)) ? 2 * qrows : rows * (D / 4);
+    hipLaunchKernelGGL((attention_fused_prepass_kernel<D>), dim3(static_cast<unsigned>((threads_pre + 255) / 256)), dim3(256), 0, stream,
             tensor(a.output, a.os), tensor(a.upstream, a.us), a.delta, a.gradient_q, a.gradient_k, a.gradient_v, shape, qrows, krows,
             split_above);
     hipError_t error = hipGetLastError();
