@@ -131,8 +131,18 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
     }
 
     // P = exp(s - m) / l = exp2(s·c2 - (m·log2e + log2 l)): the normaliser folds into the exponent offset.
-    // A row without visible keys gets offset +inf, so exp2(x - inf) = 0.
+    // A row without visible keys gets offset +inf, so exp2(x - inf) = 0. At D = 32 the offset seeds every tile's
+    // S chain and Q is pre-scaled by c2, so P = exp2(chain) (an FMA per element saved; 16 registers that the D = 64
+    // kernel has no room for).
     const float mc = m != -INFINITY ? fmaf(m, kLog2e, __log2f(l)) : INFINITY;
+    constexpr bool SEED = D == 32;
+    f32x16 seed{};
+    if constexpr (SEED) {
+#pragma unroll
+        for (int j = 0; j < 16; ++j) seed[j] = -mc;
+#pragma unroll
+        for (int c = 0; c < HALF; ++c) qr[c] *= c2;
+    }
 
     const int wlo = window_lo(s, query);
     const int whi = window_hi(s, query);
@@ -167,7 +177,7 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
             for (int t = 0; t < DT; ++t) kc[t][j] = buffer_load(kbuf, klane + 128u * t, static_cast<uint32_t>(8 * (j >> 2) + (j & 3)) * kstep);
         }
 
-        f32x16 sc{}, dp{};
+        f32x16 sc = seed, dp{};
 #pragma unroll
         for (int c = 0; c < HALF; ++c) {
             sc = mfma(kr[c], qr[c], sc);
@@ -179,7 +189,7 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
 
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-            const float p = exp2_fast(fmaf(sc[j], c2, -mc));
+            const float p = exp2_fast(SEED ? sc[j] : fmaf(sc[j], c2, -mc));
             sc[j] = p * (dp[j] - dlt);
         }
         if (bits != 0xffffffffu || !tile_in_window(s, q0, key0)) {
@@ -214,7 +224,7 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
             wave_lds_sync();
             load_raw(r, next_key0);
 
-            f32x16 sc{}, dp{};
+            f32x16 sc = seed, dp{};
             {
                 float kr[HALF];
                 read_row_layout<D>(kslot, kr);
@@ -231,7 +241,7 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
-                const float p = exp2_fast(fmaf(sc[j], c2, -mc));
+                const float p = exp2_fast(SEED ? sc[j] : fmaf(sc[j], c2, -mc));
                 sc[j] = p * (dp[j] - dlt);
             }
             const bool boundary = bits != 0xffffffffu || !tile_in_window(s, q0, key0);
@@ -389,8 +399,58 @@ __device__ __forceinline__ void dkdv_tiles(const Tensor &q, const Tensor &k, con
     if constexpr (STAGE) {
         if (range > start && limit > 0) load_raw(raw, first + start * kTile);
     }
+    // At D = 32, S·scale·log2e comes straight out of the S MFMAs: K is pre-scaled here, and every tile's S chain starts
+    // from -(m·log2e + log2 l) of its queries (-inf for queries without keys), so P = exp2(chain); the dP chain starts
+    // from -δ, so dS = P·chain. That saves an FMA and a subtraction per element and tile, and 9 registers. At D = 64
+    // the kernels with two waves per item ran 4-9% slower seeded (the schedule at 256 registers waits on every LDS
+    // read of the dO rows), so they subtract as before.
+    constexpr bool SEED = D == 32;
+    if constexpr (SEED) {
+#pragma unroll
+        for (int c = 0; c < HALF; ++c) kr[c] *= c2;
+    }
 
-    __shared__ __align__(16) float stats[WAVES][2][kTile];
+    __shared__ __align__(16) float stats[WAVES][2][kTile]; // exp2 offset (seeded: its negation) and δ (seeded: -δ)
+    // S and dP chain seeds of this wave's staged tile, in accumulator order (register j is query q0 + tile_row(j, h)).
+    auto seeds = [&](f32x16 &sc, f32x16 &dp) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const f32x4 a = *reinterpret_cast<const f32x4 *>(&stats[wave][0][8 * u + 4 * h]);
+            const f32x4 d = *reinterpret_cast<const f32x4 *>(&stats[wave][1][8 * u + 4 * h]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                sc[4 * u + i] = a[i];
+                dp[4 * u + i] = d[i];
+            }
+        }
+    };
+    // P and dS of a tile from the S and dP chains: four rows' constants at a time when not seeded (all sixteen at
+    // once would hold 24 more registers).
+    auto softmax = [&](f32x16 &sc, f32x16 &dp) __attribute__((always_inline)) {
+        if constexpr (SEED) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const float p = exp2_fast(sc[j]);
+                sc[j] = p;
+                dp[j] *= p;
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                __builtin_amdgcn_sched_barrier(0);
+                const f32x4 mcs = *reinterpret_cast<const f32x4 *>(&stats[wave][0][8 * u + 4 * h]);
+                const f32x4 dls = *reinterpret_cast<const f32x4 *>(&stats[wave][1][8 * u + 4 * h]);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int j = 4 * u + i;
+                    const float p = exp2_fast(fmaf(sc[j], c2, -mcs[i]));
+                    sc[j] = p;
+                    dp[j] = p * (dp[j] - dls[i]);
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
 
     // Fused dQ: K of this item in column layout (the B operand of dQ = dS·K, row key0 + tile_row(j, h), feature
     // 32t + col), pre-scaled by 1/√D and zero for masked keys, whatever K holds there. dS goes through the
@@ -446,8 +506,8 @@ __device__ __forceinline__ void dkdv_tiles(const Tensor &q, const Tensor &k, con
         wave_lds_sync();
         if (h == 0) {
             const bool ok = q0 + col < last && r.m != -INFINITY;
-            stats[wave][0][col] = ok ? fmaf(r.m, kLog2e, __log2f(r.l)) : INFINITY; // exp2(s·c2 - this) = P
-            stats[wave][1][col] = r.d;
+            stats[wave][0][col] = SEED ? (ok ? -fmaf(r.m, kLog2e, __log2f(r.l)) : -INFINITY) : (ok ? fmaf(r.m, kLog2e, __log2f(r.l)) : INFINITY);
+            stats[wave][1][col] = SEED ? -r.d : r.d;
         }
         wave_lds_sync();
 
@@ -466,6 +526,7 @@ __device__ __forceinline__ void dkdv_tiles(const Tensor &q, const Tensor &k, con
         }
 
         f32x16 sc{}, dp{};
+        if constexpr (SEED) seeds(sc, dp);
 #pragma unroll
         for (int c = 0; c < HALF; ++c) {
             sc = mfma(r.qr[c], kr[c], sc);
@@ -474,19 +535,7 @@ __device__ __forceinline__ void dkdv_tiles(const Tensor &q, const Tensor &k, con
         __builtin_amdgcn_sched_barrier(0);
         load_rows(next, next_q0);
         __builtin_amdgcn_sched_barrier(0);
-
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const f32x4 mcs = *reinterpret_cast<const f32x4 *>(&stats[wave][0][8 * u + 4 * h]);
-            const f32x4 dls = *reinterpret_cast<const f32x4 *>(&stats[wave][1][8 * u + 4 * h]);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int j = 4 * u + i;
-                const float p = exp2_fast(fmaf(sc[j], c2, -mcs[i]));
-                sc[j] = p;
-                dp[j] = p * (dp[j] - dls[i]);
-            }
-        }
+        softmax(sc, dp);
         if (bits != 0xffffffffu || q0 + kTile > last || !tile_in_window(s, q0, key0)) {
             const uint32_t keep = visible ? bit_range(qlo - q0, qhi - q0) >> (4 * h) : 0u;
 #pragma unroll
@@ -545,8 +594,8 @@ __device__ __forceinline__ void dkdv_tiles(const Tensor &q, const Tensor &k, con
             wave_lds_sync();
             if (h == 0) {
                 const bool ok = q0 + col < last && r.m != -INFINITY;
-                stats[wave][0][col] = ok ? fmaf(r.m, kLog2e, __log2f(r.l)) : INFINITY; // exp2(s·c2 - this) = P
-                stats[wave][1][col] = r.d;
+                stats[wave][0][col] = SEED ? (ok ? -fmaf(r.m, kLog2e, __log2f(r.l)) : -INFINITY) : (ok ? fmaf(r.m, kLog2e, __log2f(r.l)) : INFINITY);
+                stats[wave][1][col] = SEED ? -r.d : r.d;
             }
             {
                 RowTile<D> u;
@@ -558,6 +607,7 @@ __device__ __forceinline__ void dkdv_tiles(const Tensor &q, const Tensor &k, con
             load_raw(r, next_q0);
 
             f32x16 sc{}, dp{};
+            if constexpr (SEED) seeds(sc, dp);
             {
                 float qr[HALF];
                 read_row_layout<D>(qslot, qr);
@@ -573,21 +623,7 @@ __device__ __forceinline__ void dkdv_tiles(const Tensor &q, const Tensor &k, con
             }
             __builtin_amdgcn_sched_barrier(0);
 
-            // Four rows' constants at a time (all sixteen at once would hold 24 more registers).
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                __builtin_amdgcn_sched_barrier(0);
-                const f32x4 mcs = *reinterpret_cast<const f32x4 *>(&stats[wave][0][8 * u + 4 * h]);
-                const f32x4 dls = *reinterpret_cast<const f32x4 *>(&stats[wave][1][8 * u + 4 * h]);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int j = 4 * u + i;
-                    const float p = exp2_fast(fmaf(sc[j], c2, -mcs[i]));
-                    sc[j] = p;
-                    dp[j] = p * (dp[j] - dls[i]);
-                }
-            }
-            __builtin_amdgcn_sched_barrier(0);
+            softmax(sc, dp);
             if (bits != 0xffffffffu || q0 + kTile > last || !tile_in_window(s, q0, key0)) {
                 const uint32_t keep = visible ? bit_range(qlo - q0, qhi - q0) >> (4 * h) : 0u;
 #pragma unroll
