@@ -275,7 +275,10 @@ def test_radius_zero_and_single_key(device):
     assert np.abs(out - v).max() <= 1e-6
     assert np.abs(lse[..., 1] - 1.0).max() <= 1e-6
     assert np.abs(gq).max() <= 1e-5 and np.abs(gk).max() <= 1e-5
-    assert np.abs(gv - du).max() <= 1e-6
+    # dV = P·dO with P = exp2(x), x = s·scale·log2e − (m·log2e + log2 l) ideally 0: the backward forms x in one MFMA
+    # chain seeded with the offset, so x carries a few ulp of |s·scale·log2e| (up to ~10 here), P = 1 ± ~1e-6 and
+    # |dV − dO| ≤ ~1e-6·|dO|max; 1e-5 is the O tolerance, still 10x inside the gradients' relative 1e-4.
+    assert np.abs(gv - du).max() <= 1e-5
     # A single visible key: every output row is that key's value row and dV of that key is Σ_q dO.
     mask[:] = 0
     mask[0, 9] = 1
