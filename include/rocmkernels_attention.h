@@ -18,7 +18,11 @@
  *   - Return value is a hipError_t as int: 0 on success, 1 (hipErrorInvalidValue) on invalid arguments,
  *     detected before any HIP call, otherwise hipGetLastError() after the launches.
  *   - Work is enqueued asynchronously on `stream` (NULL = default stream); the library never allocates,
- *     frees or synchronises, and keeps no state.
+ *     frees or synchronises device memory, and keeps no device state. Host-side it caches what it can recompute:
+ *     each device's CU count (process-wide) and, per host thread, the work tables of the last shape it launched.
+ *   - Limits of the attention entry points: every (batch, head) sequence of every tensor, plus one 32-row tile, must
+ *     span less than 2 GiB, and token strides must be >= 0 (batch and head strides may be negative); otherwise
+ *     hipErrorInvalidValue.
  *
  * The *_ex entry points have no counterpart in the reference: they add `int flags` after `radius`, where
  * bit 0 (ROCMKERNELS_ATTENTION_CAUSAL) restricts every query to keys <= query, and, for the backward only,

@@ -98,7 +98,6 @@ inline bool plan_blocks(const long long seqs, const int nblocks, const int workg
     long long per_seq = 0;
     for (int kb = 0; kb < nblocks; ++kb) {
         costs[static_cast<size_t>(kb)] = cost(kb);
-        if (costs[static_cast<size_t>(kb)] > kMaxPieceStart + kMaxPieceTiles) return false;
         per_seq += costs[static_cast<size_t>(kb)];
     }
     const int groups = (seqs % 8 == 0 && workgroups % 8 == 0) ? 8 : 1;
@@ -131,7 +130,10 @@ inline bool plan_blocks(const long long seqs, const int nblocks, const int workg
                     items.push_back(Item{block, 0, c, false});
                     continue;
                 }
-                for (int a = 0; a < c; a += chunk) items.push_back(Item{block, a, std::min(chunk, c - a), true});
+                for (int a = 0; a < c; a += chunk) {
+                    if (a > kMaxPieceStart) return false; // the start field holds 8 bits: take the dispatch-order grid
+                    items.push_back(Item{block, a, std::min(chunk, c - a), true});
+                }
             }
         }
         // Longest first; ties by block so the plan does not depend on the sort's stability.

@@ -4,6 +4,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+
 #include <rocmkernels_attention.h>
 
 namespace rk {
@@ -37,7 +39,8 @@ struct BackwardArgs {
 
 // Buffer resources address one (batch, head) sequence with 32-bit byte offsets. Kernels read up to one 32-row
 // tile past the end (those reads return 0) and use offset 2^31 as "no row", so every sequence of every tensor,
-// padded by one tile, must span less than 2 GiB.
+// padded by one tile, must span less than 2 GiB. Offsets from the sequence start are unsigned, so the token stride
+// must be non-negative (a token-reversed view is rejected); batch and head strides may have either sign.
 inline bool sequence_fits(const int rows, const rocmkernels_strides &s, const int width) {
     const long long extent = (static_cast<long long>(rows) + 32) * s.token + width;
     return s.token >= 0 && extent * 4 < (1ll << 31);
@@ -51,12 +54,25 @@ inline bool sequence_fits(const int rows, const rocmkernels_strides &s, const in
 inline int forward_split_for(const long long items) { return items >= 8192 ? 1 : items >= 4096 ? 2 : 4; }
 inline int backward_split_for(const long long items) { return items >= 4096 ? 1 : items >= 2048 ? 2 : 4; }
 
-// Compute units of the current device (256 on MI355X).
+// Compute units of the current device (256 on MI355X), queried once per device and then read from a process-wide
+// cache (a device's CU count never changes), so a launch costs one hipGetDevice instead of an attribute query.
+constexpr int kMaxCachedDevices = 64;
 inline hipError_t compute_units(int &cus) {
+    static std::atomic<int> cached[kMaxCachedDevices] = {};
     int device = 0;
     const hipError_t error = hipGetDevice(&device);
     if (error != hipSuccess) return error;
-    return hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+    const bool cacheable = device >= 0 && device < kMaxCachedDevices;
+    if (cacheable) {
+        const int known = cached[device].load(std::memory_order_relaxed);
+        if (known > 0) {
+            cus = known;
+            return hipSuccess;
+        }
+    }
+    const hipError_t query = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+    if (query == hipSuccess && cacheable && cus > 0) cached[device].store(cus, std::memory_order_relaxed);
+    return query;
 }
 
 // Workgroups of 4 waves covering `items` items of `split` waves each.

@@ -18,4 +18,9 @@ def device():
 
     if not torch.cuda.is_available():
         pytest.fail("GPU test run without a GPU: a missing device is a failure, not a skip")
+    # The library is built for gfx950 only (as the reference's device test insists on its target arch,
+    # ROCmKernels.Tests/DeviceTests.cpp:14-25): any other device is a failure, not a silent mismatch.
+    arch = torch.cuda.get_device_properties(0).gcnArchName
+    if not arch.startswith("gfx950"):
+        pytest.fail(f"GPU tests need an MI355X (gfx950); device 0 is {arch}")
     return torch.device("cuda:0")

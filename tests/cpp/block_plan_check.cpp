@@ -65,6 +65,13 @@ static void check_plan(const long long seqs, const int queries, const int keys, 
     rk::BlockPlan plan;
     const bool ok = rk::plan_blocks(seqs, nblocks, cus, 3, [&](const int kb) { return cost[static_cast<size_t>(kb)]; }, plan, table.data());
     if (!ok) return; // the launch takes the dispatch-order grid; nothing to check here
+    for (int g = 0; g < plan.bins * plan.slots; ++g) {
+        const uint32_t e = table[static_cast<size_t>(g)];
+        if (e == rk::kNoPiece) continue;
+        const rk::Piece p = rk::unpack_piece(e);
+        CHECK(rk::pack_piece(p.block, p.start, p.count, p.partial) == e && p.start <= rk::kMaxPieceStart &&
+                        p.count <= rk::kMaxPieceTiles, "piece fields overflow (seqs=%lld L=%d)", seqs, keys);
+    }
     CHECK(plan.bins * plan.slots <= rk::kMaxPieces, "table overflow");
     std::vector<std::vector<int>> hits(static_cast<size_t>(seqs * nblocks));
     std::vector<int> pieces(static_cast<size_t>(seqs * nblocks), 0);
@@ -114,7 +121,10 @@ static void check_plan(const long long seqs, const int queries, const int keys, 
 
 int main() {
     const int shapes[][4] = {{1024, 1024, -1, 1}, {2048, 2048, -1, 1}, {8192, 8192, 256, 1}, {700, 700, 40, 1}, {40, 200, 5, 0},
-            {90, 50, 11, 1}, {1536, 1536, -1, 1}, {512, 512, 100, 0}, {1, 70, -1, 0}, {33, 33, 0, 0}, {130, 130, 17, 1}};
+            {90, 50, 11, 1}, {1536, 1536, -1, 1}, {512, 512, 100, 0}, {1, 70, -1, 0}, {33, 33, 0, 0}, {130, 130, 17, 1},
+            // Long rows: piece starts pass 255 query tiles, the width of the table's start field, so the plan must
+            // either keep every start in range or be rejected (then the launch takes the dispatch-order grid).
+            {10240, 10240, -1, 1}, {9000, 128, -1, 0}, {12288, 12288, -1, 1}};
     for (const auto &s : shapes) check_ranges(s[0], s[1], s[2], s[3]);
     const long long seqs[] = {1, 3, 8, 10, 16, 20, 24, 32, 48, 64};
     for (const auto &s : shapes) {

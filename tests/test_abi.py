@@ -100,6 +100,9 @@ BWD_OK = lambda: [_buf()] * 11  # noqa: E731
     ("rotary_fp32", [None] + FWD_OK()[1:] + [1, 1, 1, 0, S0, S0, S0, S0, None]),
     ("rotary_fp32", FWD_OK() + [1, 0, 1, 1, S0, S0, S0, S0, None]),
     ("rotary_fp32", FWD_OK() + [1, 1, -3, 0, S0, S0, S0, S0, None]),
+    # token-reversed views (negative token stride) are outside the buffer-resource addressing: rejected up front
+    ("attention_fp32_forward_flash", FWD_OK() + [1, 1, 8, 8, -1, attention.Strides(256, 256, -32), S0, S0, S0, None]),
+    ("attention64_fp32_backward", BWD_OK() + [1, 1, 8, 8, -1, S0, S0, S0, S0, attention.Strides(512, 512, -64), None]),
 ])
 def test_invalid_arguments_return_invalid_value(name, args):
     assert attention.call(name, *args) == attention.HIP_ERROR_INVALID_VALUE

@@ -404,6 +404,7 @@ def close_to(got, want, label):
     (32, 1, 20, 512, 100, False, True),
     (64, 1, 6, 1024, -1, True, True),     # d=64 pieces
     (64, 2, 3, 700, 40, True, False),     # radius band, ragged tail
+    (32, 1, 2, 10240, -1, True, False),   # piece starts would pass the table's 8-bit field: dispatch-order grid
 ])
 def test_fused_backward_long_sequences(device, width, batch, heads, length, radius, causal, pad):
     q, k, v, du = normal_case(900 + length + heads, width, batch, heads, length, length)
