@@ -11,13 +11,16 @@ FLOP accounting:
     the mask (ROCmKernels.Benchmark/src/AttentionBenchmarks.cpp:141-142,197);
   * roofline.achieved / tflops_*_visited: only (query, key) pairs inside the mask, 4*d FLOPs per pair forward and
     8*d backward -- the work the kernels actually have to do.
-Timing: W warm-up launches, then K launches captured in one HIP graph and replayed once between two HIP events on
-the launch stream (device synchronisation on both sides), so host launch gaps do not count; the same K launches
-issued eagerly from Python through ctypes are timed too (``ms_per_launch_eager``). Inputs are resident in HBM.
-Before each timed region the same launches run untimed for at least ``--settle-seconds`` of continuous load: under
-sustained work the MI355X shader clock rises from about 2.0 GHz to about 2.34 GHz within the first ~20 ms (measured
-with s_memtime against s_memrealtime inside the forward kernel; cycles per tile are unchanged), so without it the
-first timed launches would run at the lower clock. The timed launches do the full work of every step.
+Timing, after the reference harness (ROCmKernels.Benchmark/src/Harness.cpp:104-167): W warm-up launches, then
+K launches issued eagerly through ctypes between two HIP events (``ms_per_launch_eager``, host gaps included). The
+headline ``ms_per_step`` is the median over at least 20 samples (max(K, 20)); a sample flushes the caches (a 512 MiB
+write, larger than the 256 MB Infinity Cache), then replays one HIP graph of L back-to-back launches, L chosen so a
+sample lasts >= 10 ms, between two HIP events on the launch stream. ``ms_per_step_min`` and ``ms_per_step_p95`` give
+the spread. Inputs are resident in HBM. Before each timed region the same launches run untimed for at least
+``--settle-seconds`` of continuous load: under sustained work the MI355X shader clock rises from about 2.0 GHz to
+about 2.34 GHz within the first ~20 ms (measured with s_memtime against s_memrealtime inside the forward kernel; cycles
+per tile are unchanged), so without it the first timed launches would run at the lower clock. The timed launches do
+the full work of every step, and every replay's output is checked against the eager launch's.
 """
 import argparse
 import json
@@ -81,6 +84,9 @@ def make_inputs(cfg, device):
 
 
 SETTLE_SECONDS = 0.25
+SAMPLES_MIN = 20       # timed samples per measurement (the reference harness records at least 20)
+SAMPLE_MS = 10.0       # each sample is a graph of back-to-back launches lasting at least this long
+FLUSH_MIB = 512        # written before every sample: larger than the 256 MB Infinity Cache plus the 8 x 4 MB L2s
 
 
 def settle(launch, per_check=20):
@@ -96,6 +102,8 @@ def settle(launch, per_check=20):
 
 
 def time_eager(launch, steps, warmup, stream):
+    """W untimed warm-up launches, then exactly K launches issued eagerly (through ctypes, one by one) between two HIP
+    events on the launch stream, device synchronisation on both sides: ms per launch including host launch gaps."""
     import torch
 
     for _ in range(warmup):
@@ -112,37 +120,73 @@ def time_eager(launch, steps, warmup, stream):
     return start.elapsed_time(stop) / steps
 
 
-def time_graph(launch, steps, results, exact=True):
-    """K launches captured into one graph; returns ms per launch of one replay. Checks every replay output
-    against the eager result (``results`` are the eager outputs of the same launch): bit for bit, or, when
-    ``exact`` is false (atomically accumulated outputs), within 1e-5 of the largest magnitude."""
+_FLUSH = []
+
+
+def flush_caches():
+    """Overwrites a FLUSH_MIB buffer on the current stream, evicting the inputs from L2 and the Infinity Cache."""
     import torch
+
+    if not _FLUSH:
+        _FLUSH.append(torch.empty(FLUSH_MIB << 18, dtype=torch.float32, device="cuda"))
+    _FLUSH[0].fill_(1.0)
+
+
+def time_samples(launch, results, samples, exact=True):
+    """The reference harness's protocol (ROCmKernels.Benchmark/src/Harness.cpp:104-167) on HIP graphs: L launches of
+    the step, L chosen so one run lasts at least SAMPLE_MS, are captured in one graph; after a settle period every
+    sample flushes the caches, then replays the graph between two HIP events on the launch stream. Returns ms per
+    launch as the median, minimum and 95th percentile over the samples.
+
+    Every replay's outputs (``results``, first overwritten with NaN) are checked against the eager result: bit for
+    bit, or, when ``exact`` is false (atomically accumulated outputs), within 1e-5 of the largest magnitude."""
+    import numpy as np
+    import torch
+
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    for _ in range(3):
+        launch()
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(10):
+        launch()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    estimate = max(start.elapsed_time(stop) / 10, 1e-4)
+    per_sample = max(1, int(np.ceil(SAMPLE_MS / estimate)))
 
     reference = [r.clone() for r in results]
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        for _ in range(steps):
+        for _ in range(per_sample):
             launch()
-    stream = torch.cuda.current_stream()
-    start = torch.cuda.Event(enable_timing=True)
-    stop = torch.cuda.Event(enable_timing=True)
     settle(graph.replay, per_check=1)
     times = []
-    for _ in range(3):
+    for _ in range(max(samples, SAMPLES_MIN)):
         for r in results:
             r.fill_(float("nan"))
+        flush_caches()
         torch.cuda.synchronize()
         start.record(stream)
         graph.replay()
         stop.record(stream)
         torch.cuda.synchronize()
-        times.append(start.elapsed_time(stop) / steps)
+        times.append(start.elapsed_time(stop) / per_sample)
         for r, ref in zip(results, reference):
             if exact and not torch.equal(r.view(torch.int32), ref.view(torch.int32)):
                 raise RuntimeError("graph replay result differs bitwise from the eager launch")
             if not exact and float((r - ref).abs().max()) > 1e-5 * max(float(ref.abs().max()), 1e-30):
                 raise RuntimeError("graph replay result differs from the eager launch")
-    return min(times)
+    times = np.asarray(times)
+    return {"ms_per_launch": float(np.median(times)), "ms_min": float(times.min()), "ms_p95": float(np.percentile(times, 95)),
+            "samples": int(times.size), "launches_per_sample": per_sample}
+
+
+def time_graph(launch, steps, results, exact=True):
+    """Median ms per launch under the sampled protocol of time_samples (kept for the tests' and profiles' callers)."""
+    return time_samples(launch, results, steps, exact)["ms_per_launch"]
 
 
 def measure_rotary(cfg, steps, warmup):
@@ -172,33 +216,73 @@ def measure_rotary(cfg, steps, warmup):
             "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 8e12, 4), "shape": f"B{batch} H{heads} L{length} d32"}
 
 
-def cpu_baseline(seconds):
-    """The CPU oracle (a C port of the reference's CPU reference) timed on this host's cores on config 2."""
+def cpu_threads():
+    """(visible cores, threads used). The visible count is this process's CPU affinity; the threads used are capped by
+    OMP_NUM_THREADS when it is set (the GPU box exports the CPU share it grants one GPU there, and asks that worker
+    pools stay within it)."""
+    visible = len(os.sched_getaffinity(0))
+    try:
+        limit = int(os.environ.get("OMP_NUM_THREADS", "0"))
+    except ValueError:
+        limit = 0
+    return visible, (min(visible, limit) if limit > 0 else visible)
+
+
+def cpu_baseline(config, seconds):
+    """The C oracle (a C port of the reference's CPU reference, AttentionTests.cpp:28-125) on the same workload as the
+    GPU line, timed on this host: single-threaded and on every core this process may use, in the same process.
+    Configs 1-3 are run in full (config 3 forward and backward); configs 4-5 once each on all cores (forward and
+    backward), as planned for the CPU side. Returns the all-core rate in the GPU line's unit (convention TFLOP/s)."""
     import numpy as np
 
     import oracle
+
+    cfg = CONFIGS[config]
+    shape = (cfg["batch"], cfg["heads"], cfg["length"], cfg["width"])
     from rocmkernels_amd import inputs
 
-    cfg = CONFIGS[2]
-    shape = (cfg["batch"], cfg["heads"], cfg["length"], cfg["width"])
-    q, k, v = (inputs.normal(seed, shape) for seed in (101, 102, 103))
-    mask = np.ones((cfg["batch"], cfg["length"]), np.uint8)
-    threads = min(os.cpu_count() or 1, 16)
-    runs, elapsed = 0, 0.0
-    while elapsed < seconds or runs == 0:
+    q, k, v, du = (inputs.normal(seed, shape) for seed in (101, 102, 103, 104))
+    lengths = key_lengths(cfg)
+    mask = (np.arange(cfg["length"])[None, :] < lengths[:, None]).astype(np.uint8)
+    with_backward = config >= 3
+    upstream = du if with_backward else None
+    visible, threads = cpu_threads()
+
+    def run(nthreads):
         begin = time.perf_counter()
-        oracle.attention(q, k, v, mask, causal=True, threads=threads)
-        elapsed += time.perf_counter() - begin
-        runs += 1
-    per_run = elapsed / runs
-    convention = 4.0 * cfg["batch"] * cfg["heads"] * cfg["length"] ** 2 * cfg["width"]
-    return {
-        "value": round(convention / per_run / 1e12, 6),
+        oracle.attention(q, k, v, mask, upstream, radius=cfg["radius"], causal=True, threads=nthreads)
+        return time.perf_counter() - begin
+
+    def timed(nthreads, budget, once=False):
+        runs, elapsed = 0, 0.0
+        while runs == 0 or (not once and elapsed < budget):
+            elapsed += run(nthreads)
+            runs += 1
+        return elapsed / runs, runs
+
+    full = cfg["batch"] * cfg["heads"] * cfg["length"] ** 2
+    flops = (4.0 + (8.0 if with_backward else 0.0)) * full * cfg["width"]
+    pairs = visited_pairs(cfg, lengths)
+    flops_visited = (4.0 + (8.0 if with_backward else 0.0)) * pairs * cfg["width"]
+    many, many_runs = timed(threads, seconds / 2, once=config >= 4)
+    result = {
+        "value": round(flops / many / 1e12, 6),
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"full config-2 causal forward (24 x 1024 x 32) on the C oracle, {runs} run(s), {per_run * 1e3:.1f} ms/run",
+        "sample": (f"full {cfg['workload']} {'forward+backward' if with_backward else 'forward'} on the C oracle "
+                   f"(double scores, float gradients); {many_runs} run(s) on {threads} threads, {many * 1e3:.1f} ms/run"),
+        "ms_per_run_all_cores": round(many * 1e3, 3),
+        "tflops_visited_all_cores": round(flops_visited / many / 1e12, 6),
+        "host_cores_visible": visible,
+        "thread_limit": "OMP_NUM_THREADS" if threads < visible else "affinity",
     }
+    if config <= 3:
+        single, single_runs = timed(1, seconds / 2)
+        result["single_thread"] = {"ms_per_run": round(single * 1e3, 3), "runs": single_runs,
+                                   "tflops_convention": round(flops / single / 1e12, 6),
+                                   "tflops_visited": round(flops_visited / single / 1e12, 6)}
+    return result
 
 
 def forward_kernel_name(cfg, cus):
@@ -221,6 +305,18 @@ def load_traffic(kernel_key):
         return None
     with open(path) as handle:
         return json.load(handle).get(kernel_key, {}).get("hbm_bytes_per_launch")
+
+
+def rates(timing, flops_convention, flops_visited, eager=None):
+    """ms statistics of time_samples plus the TFLOP/s and roofline fraction they imply (median time)."""
+    ms = timing["ms_per_launch"]
+    out = dict(timing)
+    if eager is not None:
+        out["ms_per_launch_eager"] = eager
+    out.update(tflops_convention=flops_convention / (ms * 1e-3) / 1e12, tflops_visited=flops_visited / (ms * 1e-3) / 1e12,
+               flops_visited=flops_visited)
+    out["frac_of_fp32_mfma_peak_visited"] = out["tflops_visited"] / PEAK_FP32_MFMA_TFLOPS
+    return out
 
 
 def measure(cfg, steps, warmup, backward=True):
@@ -249,31 +345,49 @@ def measure(cfg, steps, warmup, backward=True):
     full = cfg["batch"] * cfg["heads"] * cfg["length"] ** 2
     stream = torch.cuda.current_stream()
     result = {"visited_pairs": pairs}
+    width = cfg["width"]
     eager = time_eager(forward, steps, warmup, stream)
-    graph = time_graph(forward, steps, [out, lse])
-    result["forward"] = dict(ms_per_launch=graph, ms_per_launch_eager=eager,
-                             tflops_convention=4.0 * full * cfg["width"] / (graph * 1e-3) / 1e12,
-                             tflops_visited=4.0 * pairs * cfg["width"] / (graph * 1e-3) / 1e12,
-                             flops_visited=4.0 * pairs * cfg["width"])
+    result["forward"] = rates(time_samples(forward, [out, lse], steps), 4.0 * full * width, 4.0 * pairs * width, eager)
     if backward:
         forward()
         eager = time_eager(backward_step, steps, warmup, stream)
-        graph = time_graph(backward_step, steps, list(grads))
-        result["backward"] = dict(ms_per_launch=graph, ms_per_launch_eager=eager,
-                                  tflops_convention=8.0 * full * cfg["width"] / (graph * 1e-3) / 1e12,
-                                  tflops_visited=8.0 * pairs * cfg["width"] / (graph * 1e-3) / 1e12,
-                                  flops_visited=8.0 * pairs * cfg["width"])
+        result["backward"] = rates(time_samples(backward_step, list(grads), steps), 8.0 * full * width, 8.0 * pairs * width, eager)
         backward_fused()
         eager = time_eager(backward_fused, steps, warmup, stream)
-        graph = time_graph(backward_fused, steps, list(grads), exact=False)
-        result["backward_fused"] = dict(ms_per_launch=graph, ms_per_launch_eager=eager,
-                                        tflops_convention=8.0 * full * cfg["width"] / (graph * 1e-3) / 1e12,
-                                        tflops_visited=8.0 * pairs * cfg["width"] / (graph * 1e-3) / 1e12,
-                                        flops_visited=8.0 * pairs * cfg["width"])
-    for part in ("forward", "backward", "backward_fused"):
-        if part in result:
-            result[part]["frac_of_fp32_mfma_peak_visited"] = result[part]["tflops_visited"] / PEAK_FP32_MFMA_TFLOPS
+        result["backward_fused"] = rates(time_samples(backward_fused, list(grads), steps, exact=False), 8.0 * full * width,
+                                         8.0 * pairs * width, eager)
     return result
+
+
+def measure_reference_case(steps):
+    """The reference's own benchmark workload (AttentionBenchmarks.cpp:36-43,205-209): B2 x H12 x L1024 x d32, Q = 0.5,
+    K = V = 0.25, mask all ones, radius -1, no causal mask, through its flash entry point attention_fp32_forward_flash.
+    Its published figures are for an RX 6700 (README.md:63); they are quoted beside ours for context only."""
+    import torch
+
+    from rocmkernels_amd import attention
+
+    device = torch.device("cuda:0")
+    shape = (2, 12, 1024, 32)
+    q = torch.full(shape, 0.5, device=device)
+    k = torch.full(shape, 0.25, device=device)
+    v = torch.full(shape, 0.25, device=device)
+    mask = torch.ones((2, 1024), dtype=torch.uint8, device=device)
+    out = torch.empty(shape, device=device)
+    lse = torch.empty(shape[:3] + (2,), device=device)
+
+    def launch():
+        attention.forward(q, k, v, mask, radius=-1, causal=False, output=out, lse=lse, entry="flash")
+
+    launch()
+    torch.cuda.synchronize()
+    if not bool((out == 0.25).all()):  # constant V: every output is exactly 0.25
+        raise RuntimeError("reference bench case: output is not 0.25")
+    flops = 4.0 * 24 * 1024 * 1024 * 32
+    timing = rates(time_samples(launch, [out, lse], steps), flops, flops)
+    timing["workload"] = "reference bench case: B2 x H12 x L1024 x d32, Q=0.5, K=V=0.25, no mask, not causal (flash entry)"
+    timing["reference_rx6700"] = {"ms_per_launch": 0.96, "tflops": 3.36, "source": "README.md:63 (RX 6700, gfx1031)"}
+    return {k: (round(v, 6) if isinstance(v, float) else v) for k, v in timing.items()}
 
 
 def rounded(d):
@@ -284,8 +398,9 @@ def main():
     global SETTLE_SECONDS
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=400)
-    parser.add_argument("--warmup", type=int, default=40)
+    parser.add_argument("--steps", type=int, default=20,
+                        help="eager launches timed back to back, and timed samples (at least 20) of >= 10 ms each")
+    parser.add_argument("--warmup", type=int, default=5)
     parser.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
     parser.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample length (0 skips it)")
     parser.add_argument("--settle-seconds", type=float, default=SETTLE_SECONDS,
@@ -322,6 +437,12 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(fwd["ms_per_launch"], 6),
+        "ms_per_step_min": round(fwd["ms_min"], 6),
+        "ms_per_step_p95": round(fwd["ms_p95"], 6),
+        "timing": {"samples": fwd["samples"], "launches_per_sample": fwd["launches_per_sample"],
+                   "statistic": "median over samples of ms per launch; each sample: cache flush (512 MiB write), then "
+                                "one HIP-graph replay of back-to-back launches lasting >= 10 ms, between HIP events",
+                   "eager_steps_timed": args.steps},
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -342,7 +463,9 @@ def main():
         if part in measured:
             result[part] = rounded(measured[part])
     result["rotary"] = measure_rotary(cfg, args.steps, args.warmup)
-    result["cpu_baseline"] = cpu_baseline(args.cpu_seconds) if args.cpu_seconds > 0 and args.config == 2 else None
+    if args.config == 2:
+        result["reference_bench_case"] = measure_reference_case(args.steps)
+    result["cpu_baseline"] = cpu_baseline(args.config, args.cpu_seconds) if args.cpu_seconds > 0 else None
     print(json.dumps(result), flush=True)
 
 

@@ -24,8 +24,9 @@
  *     keys outside it have score -inf and probability exactly 0 in the reference loop, so they add nothing.
  * Inputs are packed [batch][head][token][D], as the reference assumes (:48-49,61-62).
  *
- * The driver splits (batch, head) pairs over `threads` POSIX threads. Each pair is independent and its float
- * gradient accumulation order is unchanged, so results are bit-identical for any thread count.
+ * The driver splits the work over `threads` POSIX threads: whole (batch, head) pairs when gradients are wanted, and
+ * 64-query chunks of pairs for a forward only. Pairs are independent, query rows of a forward are too, and the float
+ * gradient accumulation order within a pair is unchanged, so results are bit-identical for any thread count.
  *
  * Parity pins for this file live in tests/test_oracle.py (closed forms, invariants, finite differences, an
  * independent float64 matrix formulation, and torch float64 autograd fixtures in tests/golden/).
@@ -48,7 +49,7 @@ typedef struct {
     const uint8_t *mask;
     float *output, *lse, *gq, *gk, *gv, *delta;
     int width, batch, heads, queries, keys, radius, causal;
-    int next; /* next (batch, head) pair, taken under the lock */
+    int next; /* next task (a pair, or a query chunk of one), taken under the lock */
     pthread_mutex_t lock;
 } Job;
 
@@ -64,7 +65,9 @@ static void key_window(const Job *job, const int query, int *first, int *last) {
     *last = hi;
 }
 
-static void run_pair(const Job *job, const int batch, const int head, double *scores, double *probabilities) {
+/* Queries [query_begin, query_end) of one (batch, head) pair. */
+static void run_pair(const Job *job, const int batch, const int head, const int query_begin, const int query_end, double *scores,
+        double *probabilities) {
     const int D = job->width;
     const double scale = 1.0 / sqrt((double)D);
     const size_t pair = (size_t)batch * job->heads + head;
@@ -73,7 +76,7 @@ static void run_pair(const Job *job, const int batch, const int head, double *sc
     const float *v = job->v + pair * job->keys * D;
     const uint8_t *mask = job->mask + (size_t)batch * job->keys;
 
-    for (int query = 0; query < job->queries; ++query) {
+    for (int query = query_begin; query < query_end; ++query) {
         const float *qrow = q + (size_t)query * D;
         int first, last;
         key_window(job, query, &first, &last);
@@ -137,6 +140,8 @@ static void run_pair(const Job *job, const int batch, const int head, double *sc
     }
 }
 
+enum { kForwardChunk = 64 };
+
 static void *worker(void *arg) {
     Job *job = (Job *)arg;
     double *scores = (double *)malloc(sizeof(double) * (size_t)job->keys);
@@ -146,12 +151,20 @@ static void *worker(void *arg) {
         free(probabilities);
         return (void *)1;
     }
+    /* A task is a (pair, query chunk). The backward accumulates dK/dV over all queries of a pair, so it keeps one task
+     * per pair (the float accumulation order of every gradient is then fixed); the forward's rows are independent and
+     * are cut into chunks of kForwardChunk queries, which keeps every thread busy when pairs are fewer than threads or
+     * not a multiple of them. */
+    const int chunk = job->upstream ? job->queries : kForwardChunk;
+    const int chunks = (job->queries + chunk - 1) / chunk;
     for (;;) {
         pthread_mutex_lock(&job->lock);
-        const int pair = job->next++;
+        const int task = job->next++;
         pthread_mutex_unlock(&job->lock);
-        if (pair >= job->batch * job->heads) break;
-        run_pair(job, pair / job->heads, pair % job->heads, scores, probabilities);
+        if (task >= job->batch * job->heads * chunks) break;
+        const int pair = task / chunks, part = task % chunks;
+        const int end = (part + 1) * chunk < job->queries ? (part + 1) * chunk : job->queries;
+        run_pair(job, pair / job->heads, pair % job->heads, part * chunk, end, scores, probabilities);
     }
     free(scores);
     free(probabilities);
@@ -179,7 +192,8 @@ int oracle_attention(const float *q, const float *k, const float *v, const uint8
     Job job = {q, k, v, upstream, mask, output, lse, gq, gk, gv, delta, width, batch, heads, queries, keys, radius, causal, 0,
             PTHREAD_MUTEX_INITIALIZER};
     if (threads < 1) threads = 1;
-    if (threads > batch * heads) threads = batch * heads;
+    const long long tasks = (long long)batch * heads * (upstream ? 1 : (queries + kForwardChunk - 1) / kForwardChunk);
+    if (threads > tasks) threads = (int)tasks;
     pthread_t *pool = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)threads);
     if (!pool) return -1;
     int failed = 0, started = 0;

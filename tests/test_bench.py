@@ -43,3 +43,19 @@ def test_forward_kernel_names_follow_the_launch_policy():
     assert bench.forward_kernel_name(bench.CONFIGS[1], 256) == "rk::attention_forward_kernel<32, false, true, 4, 0>"
     assert bench.forward_kernel_name(bench.CONFIGS[4], 256) == "rk::attention_forward_kernel<64, false, true, 4, 0>"
     assert bench.forward_kernel_name(bench.CONFIGS[5], 256) == "rk::attention_forward_kernel<64, false, true, 2, 0>"
+
+
+def test_cpu_baseline_reports_single_thread_and_all_core_rates():
+    # Config 1 is small enough to time here; the GPU box runs the same code on its own cores.
+    result = bench.cpu_baseline(1, 0.2)
+    visible, threads = bench.cpu_threads()
+    assert result["kind"] == "port" and result["unit"] == "TFLOP/s" and result["value"] > 0
+    assert result["cores"] == threads and result["host_cores_visible"] == visible == len(os.sched_getaffinity(0))
+    assert result["single_thread"]["runs"] >= 1 and result["single_thread"]["tflops_convention"] > 0
+
+
+def test_cpu_threads_respects_the_openmp_share(monkeypatch):
+    monkeypatch.setenv("OMP_NUM_THREADS", "1")
+    assert bench.cpu_threads()[1] == 1
+    monkeypatch.delenv("OMP_NUM_THREADS")
+    assert bench.cpu_threads()[1] == len(os.sched_getaffinity(0))
