@@ -25,11 +25,19 @@
  *     hipErrorInvalidValue.
  *
  * The *_ex entry points have no counterpart in the reference: they add `int flags` after `radius`, where
- * bit 0 (ROCMKERNELS_ATTENTION_CAUSAL) restricts every query to keys <= query, and, for the backward only,
- * bit 1 (ROCMKERNELS_ATTENTION_FUSED_BACKWARD) selects the fused backward: dQ is accumulated with FP32 atomics
- * in the same kernel as dK/dV (fewer matrix products, faster), and so are dK/dV of the key blocks whose query range
- * is split over several workgroups, so their low-order bits may differ from run to run; delta stays
- * bit-reproducible. All other bits must be zero (else hipErrorInvalidValue).
+ * bit 0 (ROCMKERNELS_ATTENTION_CAUSAL) restricts every query to keys <= query. For the backward, the flags also
+ * choose between two implementations of the same maths:
+ *   - fused: one kernel forms dK, dV and dQ from each recomputed score tile (5 matrix products per tile); dQ is
+ *     accumulated with FP32 atomics, and so are dK/dV of the key blocks whose query range is split over several
+ *     workgroups, so those values' low-order bits may differ from run to run (delta is bit-reproducible);
+ *   - deterministic: the reference's arrangement, a query-major dQ kernel and a key-major dK/dV kernel (7 matrix
+ *     products per tile, S and dP computed in both); bit-identical results run to run.
+ *   With neither bit 1 nor bit 2 set the library takes the faster one for the call: fused for inputs with 128-bit
+ *   access (16-byte aligned pointers, strides multiples of 4) and no radius window, deterministic otherwise.
+ *   Bit 1 (ROCMKERNELS_ATTENTION_FUSED_BACKWARD) asks for fused wherever it exists (under a radius window the
+ *   deterministic kernels run, which measured faster there); bit 2 (ROCMKERNELS_ATTENTION_DETERMINISTIC) asks for
+ *   deterministic. Setting both, or any other bit, returns hipErrorInvalidValue.
+ * The reference-named backward entry points always run the deterministic kernels, as the reference's do.
  */
 #ifndef ROCMKERNELS_ATTENTION_H
 #define ROCMKERNELS_ATTENTION_H
@@ -62,6 +70,7 @@ typedef struct rocmkernels_strides {
 
 #define ROCMKERNELS_ATTENTION_CAUSAL 1
 #define ROCMKERNELS_ATTENTION_FUSED_BACKWARD 2
+#define ROCMKERNELS_ATTENTION_DETERMINISTIC 4
 
 /* ---- 32-wide forward family ------------------------------------------------------------------ */
 
@@ -151,7 +160,7 @@ ROCMKERNELS_EXPORT int attention_fp32_forward_flash_ex(const float *q, const flo
         float *output, float *lse, int batch, int heads, int queries, int keys, int radius, int flags, rocmkernels_strides qs,
         rocmkernels_strides ks, rocmkernels_strides vs, rocmkernels_strides os, hipStream_t stream);
 
-/* attention_fp32_backward plus flags (bit 0 = causal, bit 1 = fused backward). */
+/* attention_fp32_backward plus flags (bit 0 = causal; bits 1 and 2 choose fused or deterministic, see above). */
 ROCMKERNELS_EXPORT int attention_fp32_backward_ex(const float *q, const float *k, const float *v, const bool *mask,
         const float *output, const float *lse, const float *upstream, float *gradient_q, float *gradient_k, float *gradient_v,
         float *delta, int batch, int heads, int queries, int keys, int radius, int flags, rocmkernels_strides qs,
@@ -162,7 +171,7 @@ ROCMKERNELS_EXPORT int attention64_fp32_forward_ex(const float *q, const float *
         float *output, float *lse, int batch, int heads, int queries, int keys, int radius, int flags, rocmkernels_strides qs,
         rocmkernels_strides ks, rocmkernels_strides vs, rocmkernels_strides os, hipStream_t stream);
 
-/* attention64_fp32_backward plus flags (bit 0 = causal, bit 1 = fused backward). */
+/* attention64_fp32_backward plus flags (bit 0 = causal; bits 1 and 2 choose fused or deterministic, see above). */
 ROCMKERNELS_EXPORT int attention64_fp32_backward_ex(const float *q, const float *k, const float *v, const bool *mask,
         const float *output, const float *lse, const float *upstream, float *gradient_q, float *gradient_k, float *gradient_v,
         float *delta, int batch, int heads, int queries, int keys, int radius, int flags, rocmkernels_strides qs,

@@ -17,6 +17,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 P, I = ctypes.c_void_p, ctypes.c_int
 CAUSAL = 1
 FUSED_BACKWARD = 2
+DETERMINISTIC = 4
 DTYPE_FLOAT32 = 0  # rocmkernels_dtype / ROCmKernels::Kernels::DType::Float32
 DTYPE_FLOAT16 = 1
 HIP_ERROR_INVALID_VALUE = 1
@@ -222,11 +223,14 @@ def statistics(q, k, mask, radius=-1, lse=None, stream=None):
 
 
 def backward(q, k, v, mask, output, lse, upstream, radius=-1, causal=False, entry="simple", code=None, grads=None, stream=None,
-             fused=False):
+             fused=False, deterministic=False):
     """dQ, dK, dV, delta of attention; gradients packed [B][H][L][D], delta [B][H][Lq].
 
-    ``fused`` selects the fused backward of the *_ex entry points (dQ accumulated with atomics: faster, but dQ's
-    low-order bits can change from run to run)."""
+    A causal mask, ``entry="ex"``, ``fused`` or ``deterministic`` go through the *_ex entry points, whose default
+    takes the faster backward for the call (the fused one, whose dQ is accumulated with atomics, wherever it exists);
+    ``fused`` asks for the fused backward, ``deterministic`` for the bit-reproducible two-kernel one. Otherwise
+    ``entry`` picks the reference entry point ("simple", "tiled", "tuned", "profile", "query_profile"), which always
+    runs the deterministic kernels."""
     torch = _torch()
     _device_check(q, k, v, mask, output, lse, upstream)
     batch, heads, queries, width = q.shape
@@ -240,9 +244,10 @@ def backward(q, k, v, mask, output, lse, upstream, radius=-1, causal=False, entr
     common = (_ptr(q), _ptr(k), _ptr(v), _ptr(mask), _ptr(output), _ptr(lse), _ptr(upstream), _ptr(gq), _ptr(gk), _ptr(gv),
               _ptr(delta), batch, heads, queries, keys, radius)
     views = (strides(q), strides(k), strides(v), strides(output), strides(upstream), _stream(stream))
-    if causal or fused:
+    if causal or fused or deterministic or entry == "ex":
         name = "attention_fp32_backward_ex" if width == 32 else "attention64_fp32_backward_ex"
-        check(name, *common, (CAUSAL if causal else 0) | (FUSED_BACKWARD if fused else 0), *views)
+        flags = (CAUSAL if causal else 0) | (FUSED_BACKWARD if fused else 0) | (DETERMINISTIC if deterministic else 0)
+        check(name, *common, flags, *views)
     elif width == 64:
         check("attention64_fp32_backward", *common, *views)
     elif entry in ("tuned", "profile", "query_profile"):

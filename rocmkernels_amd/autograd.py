@@ -5,8 +5,9 @@ the ctypes binding).
 
 ``attention_fp32(q, k, v, mask, radius, causal)`` returns O = softmax(QKᵀ/√D + mask) V for q/k/v [B][H][L][D]
 float32 CUDA tensors (D = 32 or 64). The forward keeps O and the {max, sum} statistics; the backward runs the
-library's backward entry point on them (the deterministic two-kernel backward, or with ``fused_backward=True`` the
-fused one whose dQ is accumulated with atomics). Everything runs on the GPU through the C ABI; there is no CPU path.
+library's *_ex backward entry point on them: by default the faster backward for the call (the fused one, whose dQ is
+accumulated with atomics, wherever it exists), with ``deterministic=True`` the bit-reproducible two-kernel one.
+Everything runs on the GPU through the C ABI; there is no CPU path.
 """
 import torch
 
@@ -17,7 +18,7 @@ class AttentionFP32(torch.autograd.Function):
     """Autograd Function over attention_fp32_forward_flash / attention64_fp32_forward (and their *_ex forms)."""
 
     @staticmethod
-    def forward(ctx, q, k, v, mask, radius, causal, fused_backward):
+    def forward(ctx, q, k, v, mask, radius, causal, deterministic):
         for name, t in (("q", q), ("k", k), ("v", v)):
             if t.dim() != 4 or t.dtype != torch.float32 or not t.is_cuda:
                 raise ValueError(f"{name} must be a float32 [batch][head][token][D] tensor on the GPU")
@@ -26,7 +27,7 @@ class AttentionFP32(torch.autograd.Function):
         q, k, v = (t if t.stride(-1) == 1 else t.contiguous() for t in (q, k, v))
         out, lse = attention.forward(q, k, v, mask, radius=radius, causal=causal)
         ctx.save_for_backward(q, k, v, mask, out, lse)
-        ctx.radius, ctx.causal, ctx.fused = radius, causal, fused_backward
+        ctx.radius, ctx.causal, ctx.deterministic = radius, causal, deterministic
         ctx.mark_non_differentiable(lse)
         return out, lse
 
@@ -38,15 +39,15 @@ class AttentionFP32(torch.autograd.Function):
         if grad_out.stride(-1) != 1:
             grad_out = grad_out.contiguous()
         gq, gk, gv, _ = attention.backward(q, k, v, mask, out, lse, grad_out, radius=ctx.radius, causal=ctx.causal,
-                                           fused=ctx.fused)
+                                           entry="ex", deterministic=ctx.deterministic)
         return gq, gk, gv, None, None, None, None
 
 
-def attention_fp32(q, k, v, mask=None, radius=-1, causal=False, fused_backward=False, return_lse=False):
+def attention_fp32(q, k, v, mask=None, radius=-1, causal=False, deterministic=False, return_lse=False):
     """Differentiable FP32 attention. mask: [B][keys] bool/uint8 on the GPU (None = every key visible)."""
     if mask is None:
         mask = torch.ones((q.shape[0], k.shape[2]), dtype=torch.uint8, device=q.device)
     elif mask.dtype == torch.bool:
         mask = mask.to(torch.uint8)
-    out, lse = AttentionFP32.apply(q, k, v, mask.contiguous(), int(radius), bool(causal), bool(fused_backward))
+    out, lse = AttentionFP32.apply(q, k, v, mask.contiguous(), int(radius), bool(causal), bool(deterministic))
     return (out, lse) if return_lse else out

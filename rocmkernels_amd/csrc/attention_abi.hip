@@ -46,6 +46,19 @@ int backward(const int D, const int flags, const rk::BackwardStage stage, const 
     return rk::launch_backward(D, stage, a, stream);
 }
 
+// _ex backward flags: causal, and at most one of fused / deterministic.
+bool bad_backward_flags(const int flags) {
+    constexpr int kKnown = ROCMKERNELS_ATTENTION_CAUSAL | ROCMKERNELS_ATTENTION_FUSED_BACKWARD | ROCMKERNELS_ATTENTION_DETERMINISTIC;
+    constexpr int kBoth = ROCMKERNELS_ATTENTION_FUSED_BACKWARD | ROCMKERNELS_ATTENTION_DETERMINISTIC;
+    return (flags & ~kKnown) != 0 || (flags & kBoth) == kBoth;
+}
+
+rk::BackwardStage backward_stage(const int flags) {
+    if (flags & ROCMKERNELS_ATTENTION_DETERMINISTIC) return rk::kBackwardAll;
+    if (flags & ROCMKERNELS_ATTENTION_FUSED_BACKWARD) return rk::kBackwardFused;
+    return rk::kBackwardAuto;
+}
+
 bool valid_group(const int group) {
     // Group codes accepted by the reference (Attention.hip:361-369 forward, :423-437 backward).
     return group == 2 || group == 8 || group == 4 || group == 84 || group == 164 || group == 1164 || group == 1264;
@@ -183,8 +196,8 @@ int attention_fp32_backward_ex(const float *q, const float *k, const float *v, c
         const float *upstream, float *gradient_q, float *gradient_k, float *gradient_v, float *delta, int batch, int heads, int queries,
         int keys, int radius, int flags, rocmkernels_strides qs, rocmkernels_strides ks, rocmkernels_strides vs, rocmkernels_strides os,
         rocmkernels_strides us, hipStream_t stream) {
-    if ((flags & ~(ROCMKERNELS_ATTENTION_CAUSAL | ROCMKERNELS_ATTENTION_FUSED_BACKWARD)) != 0 || radius < -1) return kInvalid;
-    return backward(32, flags, flags & ROCMKERNELS_ATTENTION_FUSED_BACKWARD ? rk::kBackwardFused : rk::kBackwardAll, q, k, v, mask, output, lse, upstream, gradient_q, gradient_k, gradient_v, delta, batch,
+    if (bad_backward_flags(flags) || radius < -1) return kInvalid;
+    return backward(32, flags, backward_stage(flags), q, k, v, mask, output, lse, upstream, gradient_q, gradient_k, gradient_v, delta, batch,
             heads, queries, keys, radius, qs, ks, vs, os, us, stream);
 }
 
@@ -199,8 +212,8 @@ int attention64_fp32_backward_ex(const float *q, const float *k, const float *v,
         const float *upstream, float *gradient_q, float *gradient_k, float *gradient_v, float *delta, int batch, int heads, int queries,
         int keys, int radius, int flags, rocmkernels_strides qs, rocmkernels_strides ks, rocmkernels_strides vs, rocmkernels_strides os,
         rocmkernels_strides us, hipStream_t stream) {
-    if ((flags & ~(ROCMKERNELS_ATTENTION_CAUSAL | ROCMKERNELS_ATTENTION_FUSED_BACKWARD)) != 0 || radius < -1) return kInvalid;
-    return backward(64, flags, flags & ROCMKERNELS_ATTENTION_FUSED_BACKWARD ? rk::kBackwardFused : rk::kBackwardAll, q, k, v, mask, output, lse, upstream, gradient_q, gradient_k, gradient_v, delta, batch,
+    if (bad_backward_flags(flags) || radius < -1) return kInvalid;
+    return backward(64, flags, backward_stage(flags), q, k, v, mask, output, lse, upstream, gradient_q, gradient_k, gradient_v, delta, batch,
             heads, queries, keys, radius, qs, ks, vs, os, us, stream);
 }
 

@@ -813,6 +813,9 @@ void launch_dkdv_mapped(const BackwardArgs &a, const int cus, hipStream_t stream
 template<int D, bool VEC>
 hipError_t run(BackwardStage stage, const BackwardArgs &a, const int cus, hipStream_t stream) {
     const int64_t kitems = static_cast<int64_t>((a.keys + kTile - 1) / kTile) * a.batch * a.heads;
+    // The fused key-block kernel needs 128-bit access; under a radius window, or without 128-bit access, the
+    // deterministic kernels measured faster.
+    if (stage == kBackwardAuto) stage = VEC && a.radius < 0 ? kBackwardFused : kBackwardAll;
     if (stage == kBackwardFused) {
         // Key-block kernel (one dQ add per element per 128 keys) unless a radius window is set: a block then streams
         // the union of its four key tiles' windows, three tiles longer than each tile's own (about 25% idle wave-steps
@@ -850,15 +853,18 @@ hipError_t launch_backward(const int D, const BackwardStage stage, const Backwar
     if (qblocks > 0x7fffffff || kblocks > 0x7fffffff || !sequence_fits(a.queries, a.qs, D) || !sequence_fits(a.keys, a.ks, D) ||
             !sequence_fits(a.keys, a.vs, D) || !sequence_fits(a.queries, a.os, D) || !sequence_fits(a.queries, a.us, D))
         return hipErrorInvalidValue;
-    if (stage == kBackwardFused && !sequence_fits(a.queries, rocmkernels_strides{0, 0, D}, D)) return hipErrorInvalidValue; // packed dQ, atomics
+    // The fused kernels address packed dQ (and dK/dV) through buffer resources: each sequence under 2 GiB.
+    const bool packed_fits = sequence_fits(a.queries, rocmkernels_strides{0, 0, D}, D) && sequence_fits(a.keys, rocmkernels_strides{0, 0, D}, D);
+    if (stage == kBackwardFused && !packed_fits) return hipErrorInvalidValue;
+    const BackwardStage chosen = stage == kBackwardAuto && !packed_fits ? kBackwardAll : stage;
     const bool vec = aligned16(a.q) && aligned16(a.k) && aligned16(a.v) && aligned16(a.output) && aligned16(a.upstream) &&
             aligned16(a.gradient_q) && aligned16(a.gradient_k) && aligned16(a.gradient_v) && strides4(a.qs) && strides4(a.ks) &&
             strides4(a.vs) && strides4(a.os) && strides4(a.us);
     int cus = 0;
     const hipError_t error = compute_units(cus);
     if (error != hipSuccess) return error;
-    if (D == 32) return vec ? run<32, true>(stage, a, cus, stream) : run<32, false>(stage, a, cus, stream);
-    return vec ? run<64, true>(stage, a, cus, stream) : run<64, false>(stage, a, cus, stream);
+    if (D == 32) return vec ? run<32, true>(chosen, a, cus, stream) : run<32, false>(chosen, a, cus, stream);
+    return vec ? run<64, true>(chosen, a, cus, stream) : run<64, false>(chosen, a, cus, stream);
 }
 
 } // namespace rk

@@ -103,6 +103,7 @@ enum BackwardStage {
     kBackwardQuery = 2,  // dQ only, reading delta
     kBackwardKeyValue = 3, // dK/dV only, reading delta
     kBackwardFused = 4,    // delta and dQ = 0, then dK/dV with dQ accumulated by atomics (not bit-reproducible)
+    kBackwardAuto = 5,     // the faster of kBackwardFused and kBackwardAll for the call
 };
 
 hipError_t launch_backward(int D, BackwardStage stage, const BackwardArgs &a, hipStream_t stream);

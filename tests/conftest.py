@@ -24,3 +24,21 @@ def device():
     if not arch.startswith("gfx950"):
         pytest.fail(f"GPU tests need an MI355X (gfx950); device 0 is {arch}")
     return torch.device("cuda:0")
+
+
+def pytest_terminal_summary(terminalreporter):
+    """Parity headroom: the checks of tests/parity.py that came closest to their tolerance in this run."""
+    try:
+        import parity
+    except ImportError:
+        return
+    if not parity.RECORDS:
+        return
+    worst = {}
+    for label, quantity, err, tol in parity.RECORDS:
+        if quantity not in worst or err / tol > worst[quantity][1] / worst[quantity][2]:
+            worst[quantity] = (label, err, tol)
+    terminalreporter.write_sep("-", f"parity headroom over {len(parity.RECORDS)} checks (largest error per quantity)")
+    for quantity in sorted(worst):
+        label, err, tol = worst[quantity]
+        terminalreporter.write_line(f"{quantity:>16}: {err:.3e} of {tol:.0e} ({100 * err / tol:5.1f}% of tolerance)  [{label}]")

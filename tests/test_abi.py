@@ -86,7 +86,9 @@ BWD_OK = lambda: [_buf()] * 11  # noqa: E731
     ("attention64_fp32_backward", [None] + BWD_OK()[1:] + [1, 1, 1, 1, -1, S0, S0, S0, S0, S0, None]),
     ("attention_fp32_forward_flash_ex", FWD_OK() + [1, 1, 1, 1, -1, 2, S0, S0, S0, S0, None]),
     ("attention_fp32_forward_flash_ex", FWD_OK() + [1, 1, 1, 1, -7, 1, S0, S0, S0, S0, None]),
-    ("attention_fp32_backward_ex", BWD_OK() + [1, 1, 1, 1, -1, 4, S0, S0, S0, S0, S0, None]),
+    ("attention_fp32_backward_ex", BWD_OK() + [1, 1, 1, 1, -1, 8, S0, S0, S0, S0, S0, None]),   # unknown flag bit
+    ("attention_fp32_backward_ex", BWD_OK() + [1, 1, 1, 1, -1, 6, S0, S0, S0, S0, S0, None]),   # fused + deterministic
+    ("attention64_fp32_backward_ex", BWD_OK() + [1, 1, 1, 1, -1, 7, S0, S0, S0, S0, S0, None]),
     ("attention_fp32_backward_ex", BWD_OK() + [1, 1, 0, 1, -1, 3, S0, S0, S0, S0, S0, None]),
     ("attention64_fp32_backward_ex", BWD_OK()[:7] + [None] + BWD_OK()[8:] + [1, 1, 1, 1, -1, 2, S0, S0, S0, S0, S0, None]),
     ("attention64_fp32_forward_ex", FWD_OK() + [1, 1, 1, 1, -1, 2, S0, S0, S0, S0, None]),
@@ -161,3 +163,34 @@ def test_autograd_binding_rejects_host_tensors():
     q = torch.zeros(1, 1, 4, 32)
     with pytest.raises(ValueError):
         autograd.attention_fp32(q, q, q, mask=torch.ones(1, 4, dtype=torch.uint8))
+
+
+def test_static_library_defines_every_declared_symbol():
+    archive = os.path.join(os.path.dirname(attention.library_path()), "libROCmKernels.Kernels.a")
+    out = subprocess.run(["nm", "--defined-only", archive], check=True, capture_output=True, text=True).stdout
+    defined = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    assert declared_symbols() <= defined
+
+
+def test_static_library_links_into_a_cpp_consumer(tmp_path):
+    # The reference's ROCmKernels.Kernels is a static library (CMakeLists.txt:117); a C++ program links this one the
+    # same way (archive + HIP runtime) and gets the throwing wrappers' behaviour.
+    archive = os.path.join(os.path.dirname(attention.library_path()), "libROCmKernels.Kernels.a")
+    binary = str(tmp_path / "static_consumer")
+    subprocess.run(["g++", "-std=c++17", "-Wall", "-Wextra", "-Werror", "-D__HIP_PLATFORM_AMD__", f"-I{INCLUDE}",
+                    "-I/opt/rocm/include", os.path.join(ROOT, "tests", "cpp", "static_consumer.cpp"), archive, "-o", binary,
+                    "-L/opt/rocm/lib", "-Wl,-rpath,/opt/rocm/lib", "-lamdhip64"], check=True, capture_output=True, text=True)
+    result = subprocess.run([binary], capture_output=True, text=True, timeout=60)
+    assert result.returncode == 0, result.stdout + result.stderr
+    assert result.stdout.count("HIP call failed") == 2
+
+
+def test_cmake_project_targets_gfx950_only():
+    # The configured build uses one offload arch, the reference's target names, and no other GPU toolchain.
+    build = os.path.join(ROOT, "build", "build.ninja")
+    with open(build) as handle:
+        text = handle.read()
+    arches = set(re.findall(r"--offload-arch=(\w+)", text))
+    assert arches == {"gfx950"}
+    assert "libROCmKernels.Kernels.a" in text and "libROCmKernels.Kernels.Shared.so" in text
+    assert "nvcc" not in text and "cuda" not in text.lower().replace("--cuda-device-only", "")

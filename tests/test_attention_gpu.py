@@ -21,10 +21,19 @@ pytestmark = pytest.mark.gpu
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
 
-def run_both(device, q, k, v, du, mask, radius=-1, causal=False, fwd="flash", bwd="simple", fcode=None, bcode=None):
+BACKWARD_MODES = ("default", "deterministic")
+
+
+def run_both(device, q, k, v, du, mask, radius=-1, causal=False, fwd="flash", bwd="simple", fcode=None, bcode=None, mode=None):
+    """Forward, then backward on the forward's O and lse. ``mode`` None: the entry named by ``bwd`` (the *_ex default
+    when causal); "default": the *_ex backward without a mode flag (fused where it exists); "deterministic": the *_ex
+    backward with ROCMKERNELS_ATTENTION_DETERMINISTIC."""
     tq, tk, tv, tdu, tm = to_dev(device, q, k, v, du, mask)
     out, lse = attention.forward(tq, tk, tv, tm, radius=radius, causal=causal, entry=fwd, code=fcode)
-    gq, gk, gv, delta = attention.backward(tq, tk, tv, tm, out, lse, tdu, radius=radius, causal=causal, entry=bwd, code=bcode)
+    if mode is not None:
+        bwd = "ex"
+    gq, gk, gv, delta = attention.backward(tq, tk, tv, tm, out, lse, tdu, radius=radius, causal=causal, entry=bwd, code=bcode,
+                                           deterministic=mode == "deterministic")
     return host(out, lse, gq, gk, gv, delta)
 
 
@@ -153,11 +162,12 @@ def test_backward_profile_stages_and_query_profile(device, sweep_case, radius):
     (64, 2, 1, 64, 200, -1, True, False),
     (64, 1, 3, 5, 7, 2, False, False),
 ])
-def test_shapes_masks_and_windows(device, width, batch, heads, queries, keys, radius, causal, pad):
+@pytest.mark.parametrize("mode", BACKWARD_MODES)
+def test_shapes_masks_and_windows(device, width, batch, heads, queries, keys, radius, causal, pad, mode):
     q, k, v, du = normal_case(400 + queries + keys, width, batch, heads, queries, keys)
     mask = padding_mask(405, batch, keys, max(1, keys // 2)) if pad else np.ones((batch, keys), np.uint8)
     want = oracle.attention(q, k, v, mask, du, radius=radius, causal=causal)
-    out, lse, gq, gk, gv, delta = run_both(device, q, k, v, du, mask, radius=radius, causal=causal)
+    out, lse, gq, gk, gv, delta = run_both(device, q, k, v, du, mask, radius=radius, causal=causal, mode=mode)
     check_forward(out, lse, want)
     check_backward(gq, gk, gv, delta, want)
 
@@ -179,24 +189,25 @@ def test_config1_cpu_reference_shape(device):
     check_backward(gq, gk, gv, delta, want)
 
 
-def test_config2_and_3_flash_24x1024x32_causal(device):
+@pytest.mark.parametrize("mode", BACKWARD_MODES)
+def test_config2_and_3_flash_24x1024x32_causal(device, mode):
     # B2 x H12 x 1024 x 32 causal: the north-star forward (config 2) and its backward (config 3), in full
     shape = (2, 12, 1024, 32)
     q, k, v, du = (inputs.normal(seed, shape) for seed in (101, 102, 103, 104))
     mask = np.ones((2, 1024), np.uint8)
     want = oracle.attention(q, k, v, mask, du, causal=True)
-    out, lse, gq, gk, gv, delta = run_both(device, q, k, v, du, mask, causal=True)
+    out, lse, gq, gk, gv, delta = run_both(device, q, k, v, du, mask, causal=True, mode=mode)
     check_forward(out, lse, want, "config 2")
-    check_backward(gq, gk, gv, delta, want, "config 3")
+    check_backward(gq, gk, gv, delta, want, f"config 3 {mode}")
 
 
-def _subset_and_invariants(device, width, batch, length, radius, mask, subset):
+def _full_and_invariants(device, width, batch, length, radius, mask, mode):
+    # Every sequence against the oracle (multithreaded on the host), plus size-independent properties.
     q, k, v, du = baseline_inputs(width, batch, length)
-    out, lse, gq, gk, gv, delta = run_both(device, q, k, v, du, mask, radius=radius, causal=True)
-    part = slice(0, subset)
-    want = oracle.attention(q[part], k[part], v[part], mask[part], du[part], radius=radius, causal=True)
-    check_forward(out[part], lse[part], want)
-    check_backward(gq[part], gk[part], gv[part], delta[part], want)
+    out, lse, gq, gk, gv, delta = run_both(device, q, k, v, du, mask, radius=radius, causal=True, mode=mode)
+    want = oracle.attention(q, k, v, mask, du, radius=radius, causal=True)
+    check_forward(out, lse, want, mode)
+    check_backward(gq, gk, gv, delta, want, mode)
     # Size-independent properties over the whole batch: Σ_k dV = Σ_q dO over attending rows, Σ_k dK = 0,
     # output rows inside the convex hull of the visible V rows (checked through |O| <= max |V|).
     attending = (lse[..., 1] > 0)[..., None]
@@ -206,15 +217,17 @@ def _subset_and_invariants(device, width, batch, length, radius, mask, subset):
     assert np.all(np.isfinite(out)) and np.all(np.isfinite(gq)) and np.all(np.isfinite(gk)) and np.all(np.isfinite(gv))
 
 
-def test_config4_64wide_causal_padding(device):
+@pytest.mark.parametrize("mode", BACKWARD_MODES)
+def test_config4_64wide_causal_padding(device, mode):
     lengths = inputs.uniform_int(105, 32, 1024, 2048)
     mask = (np.arange(2048)[None, :] < lengths[:, None]).astype(np.uint8)
-    _subset_and_invariants(device, 64, 32, 2048, -1, mask, subset=4)
+    _full_and_invariants(device, 64, 32, 2048, -1, mask, mode)
 
 
-def test_config5_64wide_radius256_causal(device):
+@pytest.mark.parametrize("mode", BACKWARD_MODES)
+def test_config5_64wide_radius256_causal(device, mode):
     mask = np.ones((16, 8192), np.uint8)
-    _subset_and_invariants(device, 64, 16, 8192, 256, mask, subset=2)
+    _full_and_invariants(device, 64, 16, 8192, 256, mask, mode)
 
 
 # ---- persistent grid: item table, 2 or 3 items per CU, per-XCD or whole-chip bins -----------------------------
@@ -226,13 +239,14 @@ def test_config5_64wide_radius256_causal(device):
     (64, 1, 8, 2048, -1, True, False),    # 512 items at d=64: 2 per CU
     (64, 3, 3, 1024, 40, True, True),     # 288 items at d=64, radius and padding, 9 sequences
 ])
-def test_persistent_grid_mappings(device, width, batch, heads, length, radius, causal, pad):
+@pytest.mark.parametrize("mode", BACKWARD_MODES)
+def test_persistent_grid_mappings(device, width, batch, heads, length, radius, causal, pad, mode):
     # On a 256-CU MI355X these shapes take the persistent forward (and, at d=32, the persistent dQ pass) with the
     # host-built item table; the forward and backward must match the oracle as on every other path.
     q, k, v, du = normal_case(700 + length + heads, width, batch, heads, length, length)
     mask = padding_mask(705, batch, length, length // 2) if pad else np.ones((batch, length), np.uint8)
     want = oracle.attention(q, k, v, mask, du, radius=radius, causal=causal)
-    out, lse, gq, gk, gv, delta = run_both(device, q, k, v, du, mask, radius=radius, causal=causal)
+    out, lse, gq, gk, gv, delta = run_both(device, q, k, v, du, mask, radius=radius, causal=causal, mode=mode)
     check_forward(out, lse, want)
     check_backward(gq, gk, gv, delta, want)
 
@@ -346,8 +360,8 @@ def test_strided_and_unaligned_inputs(device):
 def test_results_are_deterministic(device):
     q, k, v, du = normal_case(506, 32, 2, 4, 200, 200)
     mask = padding_mask(507, 2, 200, 120)
-    first = run_both(device, q, k, v, du, mask, causal=True)
-    second = run_both(device, q, k, v, du, mask, causal=True)
+    first = run_both(device, q, k, v, du, mask, causal=True, mode="deterministic")
+    second = run_both(device, q, k, v, du, mask, causal=True, mode="deterministic")
     for a, b in zip(first, second):
         assert np.array_equal(a, b, equal_nan=True)
 
@@ -355,10 +369,11 @@ def test_results_are_deterministic(device):
 # ---- fused backward (flag ROCMKERNELS_ATTENTION_FUSED_BACKWARD of the *_ex entry points) -----------------------
 
 def run_fused_and_default(device, q, k, v, du, mask, radius, causal):
+    """The fused backward (flag) and the deterministic one on the same forward."""
     tq, tk, tv, tdu, tm = to_dev(device, q, k, v, du, mask)
     out, lse = attention.forward(tq, tk, tv, tm, radius=radius, causal=causal)
     fused = attention.backward(tq, tk, tv, tm, out, lse, tdu, radius=radius, causal=causal, fused=True)
-    default = attention.backward(tq, tk, tv, tm, out, lse, tdu, radius=radius, causal=causal)
+    default = attention.backward(tq, tk, tv, tm, out, lse, tdu, radius=radius, causal=causal, deterministic=True)
     return host(out, lse, *fused), host(*default)
 
 
@@ -464,3 +479,33 @@ def test_fused_backward_config4_subset(device):
     want = oracle.attention(q[part], k[part], v[part], mask[part], du[part], causal=True)
     check_backward(gq[part], gk[part], gv[part], delta[part], want, "config 4 fused")
     assert np.all(np.isfinite(gq))
+
+
+# ---- large logits: peaked softmax rows, as trained attention produces them ------------------------------------
+
+@pytest.mark.parametrize("width,batch,heads,length,gain,radius,causal", [
+    (32, 2, 3, 300, 4.0, -1, True),
+    (32, 2, 3, 300, 6.0, -1, True),
+    (64, 2, 3, 300, 4.0, -1, True),
+    (64, 2, 3, 300, 6.0, -1, True),
+    (32, 1, 4, 200, 5.0, 20, False),     # radius band, not causal
+    (64, 2, 2, 260, 5.0, 33, True),      # band inside the causal mask
+    (32, 2, 12, 1024, 5.0, -1, True),    # config-2 shape: persistent grids
+    (64, 4, 1, 2048, 4.0, -1, True),     # config-4 rows
+])
+@pytest.mark.parametrize("mode", BACKWARD_MODES)
+def test_large_logits(device, width, batch, heads, length, gain, radius, causal, mode):
+    # Q and K scaled by `gain`: scores q.k/sqrt(D) have standard deviation gain^2 (16 to 36), so row maxima reach the
+    # tens to a hundred and each row's softmax is dominated by a few keys. The forward, and the backward (fused by
+    # default, and the deterministic kernels), must still meet O <= 1e-5 and gradients <= 1e-4.
+    q, k, v, du = normal_case(1100 + length + int(gain), width, batch, heads, length, length)
+    q *= gain
+    k *= gain
+    mask = np.ones((batch, length), np.uint8)
+    want = oracle.attention(q, k, v, mask, du, radius=radius, causal=causal)
+    out, lse, gq, gk, gv, delta = run_both(device, q, k, v, du, mask, radius=radius, causal=causal, mode=mode)
+    peak = float(np.abs(want["lse"][..., 0]).max())
+    assert peak > 10.0, f"row maxima only reach {peak:.1f}"
+    label = f"gain {gain} (row max up to {peak:.0f}) {mode}"
+    check_forward(out, lse, want, label)
+    check_backward(gq, gk, gv, delta, want, label)
