@@ -4,7 +4,7 @@
   dQ/dK/dV: max|got - want| / max|want| <= 1e-4 (normwise over the tensor);  delta: max-abs <= 1e-5 * max(1, max|delta|).
 Beside the normwise gradient error every check also measures the per-row one, max over rows of
 max|got - want| / max|want| within the row (rows whose largest |want| is under 1e-3 of the tensor's largest use that
-floor instead), and asserts it <= ROW_TOL. Every check records its margins in RECORDS; tests/conftest.py prints the
+floor instead; an all-zero expected tensor uses 1, as rel() does), and asserts it <= ROW_TOL. Every check records its margins in RECORDS; tests/conftest.py prints the
 tightest ones at the end of the run.
 """
 import os
@@ -33,7 +33,8 @@ def row_rel(a, b):
     a = np.asarray(a, dtype=np.float64)
     b = np.asarray(b, dtype=np.float64)
     scale = np.abs(b).max(axis=-1)
-    floor = ROW_FLOOR * max(float(np.abs(b).max(initial=0.0)), 1e-30)
+    largest = float(np.abs(b).max(initial=0.0))
+    floor = ROW_FLOOR * largest if largest > 0 else 1.0  # an all-zero tensor is judged in absolute terms, as by rel()
     err = np.abs(a - b).max(axis=-1) / np.maximum(scale, floor)
     return float(err.max(initial=0.0))
 
@@ -43,29 +44,36 @@ def record(label, quantity, err, tol):
     RECORDS.append((f"{test} {label}".strip(), quantity, float(err), float(tol)))
 
 
-def check_forward(output, lse, want, label=""):
+def check_forward(output, lse, want, label="", floor=None):
+    """O, lse max and lse sum against the oracle at O_TOL, or, given ``floor`` (fp32_score_floor of the inputs), at
+    max(O_TOL, 2 x floor) for each."""
     output = np.asarray(output)
     lse = np.asarray(lse)
+    tol = {key: max(O_TOL, 2.0 * floor[key]) if floor else O_TOL for key in ("output", "lse_max", "lse_sum")}
+    suffix = ", FP32 score floor" if floor else ""
     err = np.abs(output.astype(np.float64) - want["output"]).max()
-    record(label, "O max-abs", err, O_TOL)
-    assert err <= O_TOL, f"{label} O max-abs {err:.3e}"
+    record(label, "O max-abs" + suffix, err, tol["output"])
+    assert err <= tol["output"], f"{label} O max-abs {err:.3e}"
     finite = np.isfinite(np.asarray(want["lse"])[..., 0])
     assert np.array_equal(np.isfinite(lse[..., 0]), finite), f"{label} lse finiteness"
     err_m = np.abs(lse[..., 0][finite] - want["lse"][..., 0][finite]).max(initial=0.0)
-    assert err_m <= O_TOL, f"{label} lse max max-abs {err_m:.3e}"
+    record(label, "lse max" + suffix, err_m, tol["lse_max"])
+    assert err_m <= tol["lse_max"], f"{label} lse max max-abs {err_m:.3e}"
     assert np.all(lse[..., 1][~finite] == 0.0)
     err_s = rel(lse[..., 1], want["lse"][..., 1])
-    assert err_s <= O_TOL, f"{label} lse sum rel {err_s:.3e}"
+    record(label, "lse sum" + suffix, err_s, tol["lse_sum"])
+    assert err_s <= tol["lse_sum"], f"{label} lse sum rel {err_s:.3e}"
 
 
-def check_backward(gq, gk, gv, delta, want, label=""):
+def check_backward(gq, gk, gv, delta, want, label="", row_tol=ROW_TOL):
+    """Gradients at G_TOL normwise and ``row_tol`` per row (see the module docstring), delta at O_TOL."""
     for name, got in (("gq", gq), ("gk", gk), ("gv", gv)):
         err = rel(got, want[name])
         row = row_rel(got, want[name])
         record(label, f"{name} normwise", err, G_TOL)
-        record(label, f"{name} per-row", row, ROW_TOL)
+        record(label, f"{name} per-row" + (" (peaked rows)" if row_tol != ROW_TOL else ""), row, row_tol)
         assert err <= G_TOL, f"{label} {name} rel {err:.3e}"
-        assert row <= ROW_TOL, f"{label} {name} per-row rel {row:.3e}"
+        assert row <= row_tol, f"{label} {name} per-row rel {row:.3e}"
     if delta is not None and "delta" in want:
         scale = max(1.0, float(np.abs(want["delta"]).max()))
         err = np.abs(np.asarray(delta, np.float64) - want["delta"]).max()
@@ -92,3 +100,40 @@ def normal_case(seed, width, batch, heads, queries, keys):
 def padding_mask(seed, batch, keys, low):
     lengths = inputs.uniform_int(seed, batch, low, keys)
     return (np.arange(keys)[None, :] < lengths[:, None]).astype(np.uint8)
+
+
+def fp32_score_floor(q, k, v, mask, radius=-1, causal=False):
+    """Error of an FP32 forward whose scores are plain FP32 dot products: each score q.k accumulated feature by feature
+    with one rounding per fused multiply-add (the reference GPU kernels' own arithmetic), everything after it in
+    float64. Returns a dict with the largest |O - O_exact| ("output"), |max - max_exact| ("lse_max") and relative sum
+    error ("lse_sum"). With large logits it passes O_TOL (row maxima near 45 give about 6e-6 to 1.2e-5 on O, near 180
+    about 3e-5 on N(0,1) values), so tests of such inputs bound the GPU forward by a multiple of it."""
+    q = np.asarray(q, np.float32)
+    k = np.asarray(k, np.float32)
+    v = np.asarray(v, np.float64)
+    queries, keys, width = q.shape[2], k.shape[2], q.shape[3]
+    exact = np.einsum("bhqd,bhkd->bhqk", q.astype(np.float64), k.astype(np.float64)) / np.sqrt(width)
+    rounded = np.zeros(q.shape[:3] + (keys,), np.float32)
+    for c in range(width):
+        rounded = (rounded.astype(np.float64) + q[..., c, None].astype(np.float64) * k[..., None, :, c]).astype(np.float32)
+    rounded = rounded.astype(np.float64) / np.sqrt(width)
+    qi, ki = np.arange(queries)[:, None], np.arange(keys)[None, :]
+    visible = np.ones((queries, keys), bool)
+    if causal:
+        visible &= ki <= qi
+    if radius >= 0:
+        visible &= np.abs(qi - ki) <= radius
+    visible = visible[None, None] & (np.asarray(mask) != 0)[:, None, None, :]
+
+    def forward(scores):
+        scores = np.where(visible, scores, -np.inf)
+        m = scores.max(-1, keepdims=True)
+        p = np.where(visible, np.exp(scores - np.where(np.isfinite(m), m, 0.0)), 0.0)
+        total = p.sum(-1, keepdims=True)
+        return (p / np.where(total > 0, total, 1.0)) @ v, m[..., 0], total[..., 0]
+
+    o, m, total = forward(exact)
+    o32, m32, total32 = forward(rounded)
+    finite = np.isfinite(m)
+    return {"output": float(np.abs(o32 - o).max()), "lse_max": float(np.abs(m32 - m)[finite].max(initial=0.0)),
+            "lse_sum": float((np.abs(total32 - total) / np.where(total > 0, total, 1.0)).max())}

@@ -1,13 +1,14 @@
 """GPU run of the namespaced C++ wrappers (include/ROCmKernels/...), the layer the reference's own tests call
 (ROCmKernels.Tests/AttentionTests.cpp:162-224,254-264).
 
-tests/cpp/wrapper_gpu_check.cpp (built by the CMake project next to the library) calls every wrapper once on device
-buffers: Q and V token-major, K, dO and the outputs packed, so swapped or dropped stride and pointer arguments change
-the results. This test writes its inputs, runs it, makes the same calls through the C entry points (ctypes) and
+tests/cpp/wrapper_gpu_check.cpp (built by the CMake project next to the library as librocmkernels_wrapper_gpu_check.so)
+calls every wrapper once on device buffers: Q and V token-major, K, dO and the outputs packed, so swapped or dropped
+stride and pointer arguments change the results. This test writes its inputs, calls it in this process through ctypes
+(a process that has initialised the GPU starts no other program), makes the same calls through the C entry points and
 requires every output to match bit for bit; a few are also checked against the CPU oracle.
 """
+import ctypes
 import os
-import subprocess
 
 import numpy as np
 import pytest
@@ -20,7 +21,7 @@ from rocmkernels_amd import attention, inputs
 pytestmark = pytest.mark.gpu
 
 B, H, L = 2, 3, 70
-PROGRAM = os.path.join(os.path.dirname(attention.library_path()), "wrapper_gpu_check")
+CHECK_LIBRARY = os.path.join(os.path.dirname(attention.library_path()), "librocmkernels_wrapper_gpu_check.so")
 
 
 def _tensors(device):
@@ -45,13 +46,20 @@ def _token_major(device, a):
 
 
 def test_cpp_wrappers_match_c_entry_points(device, tmp_path):
-    if not os.path.exists(PROGRAM):
-        pytest.fail(f"{PROGRAM} is missing: build it with __graft_entry__.build() (CMake)")
+    if not os.path.exists(CHECK_LIBRARY):
+        pytest.fail(f"{CHECK_LIBRARY} is missing: build it with __graft_entry__.build() (CMake)")
     data = _tensors(device)
     for name, a in data.items():
-        a.tofile(tmp_path / name)
-    run = subprocess.run([PROGRAM, str(tmp_path), str(B), str(H), str(L)], capture_output=True, text=True, timeout=120)
-    assert run.returncode == 0, run.stdout + run.stderr
+        # Q and V files hold the token-major storage [B][L][H][D] the program views through strides.
+        stored = a.transpose(0, 2, 1, 3) if name in ("q32", "v32", "q64", "v64") else a
+        np.ascontiguousarray(stored).tofile(tmp_path / name)
+    attention.lib()  # the library the wrappers call is the one the ctypes calls below use
+    check_library = ctypes.CDLL(CHECK_LIBRARY)
+    check_library.wrapper_gpu_check.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    check_library.wrapper_gpu_check.restype = ctypes.c_int
+    torch.cuda.synchronize()
+    written = check_library.wrapper_gpu_check(str(tmp_path).encode(), B, H, L)
+    assert written > 0, "wrapper_gpu_check failed (see stderr)"
 
     def out(name, shape, dtype=np.float32):
         return np.fromfile(tmp_path / f"out_{name}", dtype=dtype).reshape(shape)
@@ -68,9 +76,12 @@ def test_cpp_wrappers_match_c_entry_points(device, tmp_path):
     def same(name, got_device, shape, dtype=np.float32):
         nonlocal checked
         torch.cuda.synchronize()
-        want = got_device.cpu().numpy()
+        want = np.ascontiguousarray(got_device.cpu().numpy())
         got = out(name, shape, dtype)
-        assert got.tobytes() == np.ascontiguousarray(want).tobytes(), f"{name}: wrapper and C entry point differ"
+        identical = got.tobytes() == want.tobytes()
+        if not identical:
+            differ = int((got.view(np.uint8) != want.view(np.uint8)).sum())
+            pytest.fail(f"{name}: wrapper and C entry point differ in {differ} bytes")
         checked += 1
 
     forward_cases = [("forward", "simple", -1, None), ("forward_tiled", "tiled", 5, None), ("forward_flash", "flash", -1, None),
@@ -121,7 +132,7 @@ def test_cpp_wrappers_match_c_entry_points(device, tmp_path):
         rq, rk = attention.rotary(q32, k32, cos, sin, backward=backward)
         same(f"{name}_q", rq, (B, L, H, 32))
         same(f"{name}_k", rk, (B, L, H, 32))
-    assert checked == 49 and f"{checked} outputs written" in run.stdout  # every wrapper output compared
+    assert checked == written == 49  # every wrapper output compared
 
     # The wrapper outputs also meet the oracle (the C entry points' parity is covered in test_attention_gpu.py).
     want = oracle.attention(data["q32"], data["k32"], data["v32"], data["mask"], data["u32"])
