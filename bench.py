@@ -164,7 +164,7 @@ def time_samples(launch, results, samples, exact=True):
             launch()
     settle(graph.replay, per_check=1)
     times = []
-    for _ in range(max(samples, SAMPLES_MIN)):
+    for _ in range(max(samples, SAMPLES_MIN)):  # SAMPLES_MIN is lowered only for short profiler runs (--samples)
         for r in results:
             r.fill_(float("nan"))
         flush_caches()
@@ -335,11 +335,11 @@ def measure(cfg, steps, warmup, backward=True):
     def forward():
         attention.forward(q, k, v, mask, radius=cfg["radius"], causal=True, output=out, lse=lse)
 
-    def backward_step():
+    def backward_step():  # the _ex default: the faster backward for the call (fused where it exists)
         attention.backward(q, k, v, mask, out, lse, du, radius=cfg["radius"], causal=True, grads=grads)
 
-    def backward_fused():
-        attention.backward(q, k, v, mask, out, lse, du, radius=cfg["radius"], causal=True, grads=grads, fused=True)
+    def backward_deterministic():
+        attention.backward(q, k, v, mask, out, lse, du, radius=cfg["radius"], causal=True, grads=grads, deterministic=True)
 
     pairs = visited_pairs(cfg, lengths)
     full = cfg["batch"] * cfg["heads"] * cfg["length"] ** 2
@@ -349,13 +349,16 @@ def measure(cfg, steps, warmup, backward=True):
     eager = time_eager(forward, steps, warmup, stream)
     result["forward"] = rates(time_samples(forward, [out, lse], steps), 4.0 * full * width, 4.0 * pairs * width, eager)
     if backward:
+        # The default backward may accumulate dQ with atomics (checked against the eager result within 1e-5); the
+        # deterministic one is checked bit for bit.
         forward()
         eager = time_eager(backward_step, steps, warmup, stream)
-        result["backward"] = rates(time_samples(backward_step, list(grads), steps), 8.0 * full * width, 8.0 * pairs * width, eager)
-        backward_fused()
-        eager = time_eager(backward_fused, steps, warmup, stream)
-        result["backward_fused"] = rates(time_samples(backward_fused, list(grads), steps, exact=False), 8.0 * full * width,
-                                         8.0 * pairs * width, eager)
+        result["backward"] = rates(time_samples(backward_step, list(grads), steps, exact=False), 8.0 * full * width,
+                                   8.0 * pairs * width, eager)
+        backward_deterministic()
+        eager = time_eager(backward_deterministic, steps, warmup, stream)
+        result["backward_deterministic"] = rates(time_samples(backward_deterministic, list(grads), steps), 8.0 * full * width,
+                                                 8.0 * pairs * width, eager)
     return result
 
 
@@ -395,7 +398,7 @@ def rounded(d):
 
 
 def main():
-    global SETTLE_SECONDS
+    global SETTLE_SECONDS, SAMPLES_MIN, SAMPLE_MS
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=20,
@@ -406,6 +409,9 @@ def main():
     parser.add_argument("--settle-seconds", type=float, default=SETTLE_SECONDS,
                         help="untimed continuous load before each timed region (sustained shader clock)")
     parser.add_argument("--no-backward", action="store_true")
+    parser.add_argument("--samples", type=int, default=SAMPLES_MIN,
+                        help="timed samples per measurement (default 20, the harness's minimum; fewer only for profiler runs)")
+    parser.add_argument("--sample-ms", type=float, default=SAMPLE_MS, help="minimum length of one sample in ms")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
                         help="first copy a buffer of this many MiB on the device (reference for rocprofv3 byte counters)")
     args = parser.parse_args()
@@ -425,6 +431,8 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     SETTLE_SECONDS = args.settle_seconds
+    SAMPLES_MIN = max(1, args.samples)
+    SAMPLE_MS = args.sample_ms
     cfg = CONFIGS[args.config]
     measured = measure(cfg, args.steps, args.warmup, backward=not args.no_backward)
     fwd = measured["forward"]
@@ -459,7 +467,7 @@ def main():
                      "traffic": load_traffic(f"{kernel} config{args.config}"), "kernel": kernel,
                      "flops_per_launch": fwd["flops_visited"]},
     }
-    for part in ("backward", "backward_fused"):
+    for part in ("backward", "backward_deterministic"):
         if part in measured:
             result[part] = rounded(measured[part])
     result["rotary"] = measure_rotary(cfg, args.steps, args.warmup)
