@@ -299,12 +299,36 @@ def forward_kernel_name(cfg, cus):
     return f"rk::attention_forward_kernel<{cfg['width']}, false, true, {split}, 0>"
 
 
-def load_traffic(kernel_key):
+def traffic_table():
     path = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(path):
-        return None
+        return {}
     with open(path) as handle:
-        return json.load(handle).get(kernel_key, {}).get("hbm_bytes_per_launch")
+        return json.load(handle)
+
+
+def profile_config(config):
+    """Configs 2 and 3 share their workload (forward at config 2, backward at config 3), profiled together as config 2."""
+    return 2 if config == 3 else config
+
+
+def load_traffic(kernel, config):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter summary (profiles/traffic.json), or None."""
+    return traffic_table().get(f"{kernel} config{profile_config(config)}", {}).get("hbm_bytes_per_launch")
+
+
+def backward_traffic(config, part):
+    """HBM and algorithmic bytes per launch of the kernels one backward call runs, from profiles/traffic.json: the fused
+    pre-pass and kernel for the default backward where the library takes it (no radius window), the dQ and dK/dV
+    kernels otherwise and for the deterministic backward."""
+    suffix = f" config{profile_config(config)}"
+    rows = {k[:-len(suffix)]: v for k, v in traffic_table().items() if k.endswith(suffix) and "forward_kernel" not in k}
+    fused = part == "backward" and CONFIGS[config]["radius"] < 0
+    names = sorted(n for n in rows if ("fused" in n) == fused)
+    if not names:
+        return None
+    return {"kernels": names, "hbm_bytes_per_launch": sum(rows[n]["hbm_bytes_per_launch"] for n in names),
+            "algorithmic_bytes_per_launch": sum(rows[n]["algorithmic_bytes_per_launch"] for n in names)}
 
 
 def rates(timing, flops_convention, flops_visited, eager=None):
@@ -464,12 +488,13 @@ def main():
         "ms_per_launch_eager": round(fwd["ms_per_launch_eager"], 6),
         "roofline": {"bound": "mfma", "achieved": round(fwd["tflops_visited"], 4), "peak": PEAK_FP32_MFMA_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(fwd["tflops_visited"] / PEAK_FP32_MFMA_TFLOPS, 4),
-                     "traffic": load_traffic(f"{kernel} config{args.config}"), "kernel": kernel,
+                     "traffic": load_traffic(kernel, args.config), "kernel": kernel,
                      "flops_per_launch": fwd["flops_visited"]},
     }
     for part in ("backward", "backward_deterministic"):
         if part in measured:
             result[part] = rounded(measured[part])
+            result[part]["traffic"] = backward_traffic(args.config, part)
     result["rotary"] = measure_rotary(cfg, args.steps, args.warmup)
     if args.config == 2:
         result["reference_bench_case"] = measure_reference_case(args.steps)
