@@ -320,18 +320,34 @@ struct WorkItem {
     bool valid;
 };
 
+//
+// When the sequences and the grid split evenly over the 8 XCDs (workgroup g runs on XCD g mod 8), XCD x takes the
+// sequences x, x + 8, ... only, still rank-major within them: every XCD then streams the K/V (or Q/dO) rows of a quarter
+// or less of the sequences from its own L2, instead of every sequence at every other rank.
 template<int SPLIT>
 __device__ __forceinline__ WorkItem work_item(const Shape &s, const int tiles_per_seq) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave); // wave-uniform: keeps tile bookkeeping scalar
     const int seqs = s.batch * s.heads;
-    const int item = blockIdx.x * (kWaves / SPLIT) + wave / SPLIT;
+    constexpr int PER_GROUP = kWaves / SPLIT;
+    const int items = seqs * tiles_per_seq;
+    const bool by_xcd = seqs % 8 == 0 && gridDim.x % 8 == 0 && static_cast<int64_t>(gridDim.x) * PER_GROUP == items;
     WorkItem w;
     w.sub = wave % SPLIT;
     w.split = SPLIT;
     w.lead = w.sub;
-    w.valid = item < seqs * tiles_per_seq;
-    w.rank = item / seqs;
-    w.seq = item - w.rank * seqs;
+    if (by_xcd) {
+        const int xcd = static_cast<int>(blockIdx.x) & 7;
+        const int local = (static_cast<int>(blockIdx.x) >> 3) * PER_GROUP + wave / SPLIT; // item index within the XCD
+        const int own = seqs >> 3;                                                         // sequences of the XCD
+        w.valid = true;
+        w.rank = local / own;
+        w.seq = xcd + 8 * (local - w.rank * own);
+    } else {
+        const int item = blockIdx.x * PER_GROUP + wave / SPLIT;
+        w.valid = item < items;
+        w.rank = item / seqs;
+        w.seq = item - w.rank * seqs;
+    }
     w.b = w.seq / s.heads;
     w.head = w.seq - w.b * s.heads;
     return w;
