@@ -33,10 +33,10 @@
  *   - deterministic: the reference's arrangement, a query-major dQ kernel and a key-major dK/dV kernel (7 matrix
  *     products per tile, S and dP computed in both); bit-identical results run to run.
  *   With neither bit 1 nor bit 2 set the library takes the faster one for the call: fused for inputs with 128-bit
- *   access (16-byte aligned pointers, strides multiples of 4) and no radius window, deterministic otherwise.
- *   Bit 1 (ROCMKERNELS_ATTENTION_FUSED_BACKWARD) asks for fused wherever it exists (under a radius window the
- *   deterministic kernels run, which measured faster there); bit 2 (ROCMKERNELS_ATTENTION_DETERMINISTIC) asks for
- *   deterministic. Setting both, or any other bit, returns hipErrorInvalidValue.
+ *   access (16-byte aligned pointers, strides multiples of 4) except under a radius window at head width 32,
+ *   deterministic otherwise. Bit 1 (ROCMKERNELS_ATTENTION_FUSED_BACKWARD) asks for fused wherever it exists (inputs
+ *   with 128-bit access); bit 2 (ROCMKERNELS_ATTENTION_DETERMINISTIC) asks for deterministic. Setting both, or any
+ *   other bit, returns hipErrorInvalidValue.
  * The reference-named backward entry points always run the deterministic kernels, as the reference's do.
  */
 #ifndef ROCMKERNELS_ATTENTION_H

@@ -813,18 +813,18 @@ void launch_dkdv_mapped(const BackwardArgs &a, const int cus, hipStream_t stream
 template<int D, bool VEC>
 hipError_t run(BackwardStage stage, const BackwardArgs &a, const int cus, hipStream_t stream) {
     const int64_t kitems = static_cast<int64_t>((a.keys + kTile - 1) / kTile) * a.batch * a.heads;
-    // The fused key-block kernel needs 128-bit access; under a radius window, or without 128-bit access, the
-    // deterministic kernels measured faster.
-    if (stage == kBackwardAuto) stage = VEC && a.radius < 0 ? kBackwardFused : kBackwardAll;
+    // The fused key-block kernels need 128-bit access; without it the deterministic kernels measured faster.
+    // Auto takes the fused kernels wherever they exist (128-bit access) and measured faster: under a radius window at
+    // D = 32 the band kernel did not (16 sequences x 8192 tokens, radius 256, causal: 149 us against 146 us for the
+    // deterministic pair; at D = 64 276 us against 287 us).
+    if (stage == kBackwardAuto) stage = VEC && (a.radius < 0 || D == 64) ? kBackwardFused : kBackwardAll;
     if (stage == kBackwardFused) {
-        // Key-block kernel (one dQ add per element per 128 keys) unless a radius window is set: a block then streams
-        // the union of its four key tiles' windows, three tiles longer than each tile's own (about 25% idle wave-steps
-        // at radius 256). Under a radius window the deterministic kernels, with staged tiles, measured fastest
-        // (config 5: 299 us, against 305 for the per-tile fused kernel and 331 for the key-block kernel), so the flag
-        // runs them: their results are also reproducible, which the flag allows but does not promise.
+        // Key-block kernels (one dQ add per element per 128 keys): without a radius window the piece-planned one; under a
+        // radius window the band kernel, whose skewed walk visits each key tile's own band only (the key-block walk over
+        // the union of the four bands idles a quarter of its wave-steps at radius 256).
         if constexpr (VEC) {
             if (a.radius < 0) return launch_fused_backward(D, a, cus, stream);
-            stage = kBackwardAll; // the deterministic kernels below
+            return launch_band_backward(D, a, cus, stream);
         } else {
             // Without 128-bit access: delta and dQ = 0, then the per-key-tile dK/dV kernel adding dQ per 32 x 32 tile.
             launch_dq<D, kDeltaZeroDq, VEC, 1>(a, stream);

@@ -1,0 +1,404 @@
+// Fused FP32 attention backward for radius windows on gfx950 (MI355X), head width 32 or 64, inputs with 128-bit
+// access. The maths is the reference's backward (Attention.hip:32-169, Attention64.hip:34-191): P = exp(s - max)/sum from
+// the forward's lse, δ = Σ dO·O, dS = P(dP - δ), dQ = Σ_k dS·k/√D, dK = Σ_q dS·q/√D, dV = Σ_q P·dO.
+//
+// Under a radius window every 32-key tile sees a band of query tiles that starts one tile later for each key tile: at
+// radius 256 under the causal mask key tile kt sees query tiles kt .. kt + 8. A workgroup owns a key block (128 keys, four
+// key tiles, one per wave, as in the key-block fused kernel) and walks the band skewed: at step i wave w works on query
+// tile base + i + w, so every wave meets exactly the query tiles of its own band and a block takes 9 steps there instead
+// of the 12 that a walk over the union of the four bands takes (a quarter of the wave-steps would see no key).
+//
+// Per step each wave stages nothing of its own: the four query tiles a step reads (and the one loaded for the next step,
+// a quarter by each wave, whole 128-byte lines) sit in a ring of five LDS slots, row-major; the row layouts (S and dP A
+// operands) and the column layouts (dVᵀ and dKᵀ A operands) are read from them. Each wave then computes, for its key tile
+// and its query tile,
+//   S = Q·Kᵀ and dP = dO·Vᵀ (v_mfma_f32_32x32x2f32, keys on lanes; the chains start from -(m·log2e + log2 l) and -δ,
+//   so P = exp2(S chain) and dS = P·(dP chain)), dVᵀ += dOᵀ·P and dKᵀ += Qᵀ·dS,
+// and its own share of dQ for the query tile, dQᵀ = Kᵀ·dSᵀ over its 32 keys: dS goes through the wave's transpose buffer
+// in LDS (queries onto lanes), K's column layout is held in registers (pre-scaled by 1/√D, zero for masked keys). The
+// share is summed in the query tile's slot of a second ring of five LDS tiles. Within a step the four waves work on four
+// different query tiles, and query tile T meets wave 3, 2, 1 and 0 in four consecutive steps, so the sum needs no atomics
+// (LDS float atomics cost several times the step's MFMAs): the first wave to reach the tile (wave 3, or any wave at the
+// walk's first step, since the earlier waves' bands cannot hold it) stores its share, zero when its key tile does not see
+// the query tile, and each later wave loads the partial sum as the start of its dQ chain and stores the result. The last
+// contribution comes from wave 0 at step (tile - base); after that step's barrier the four waves add the slot to dQ with
+// FP32 buffer atomics (one add per dQ element per key block, as in the key-block kernel). Blocks are never split: dK
+// and dV are stored once.
+//
+// Work mapping: one persistent workgroup per CU walks the blocks g, g + G, ...; with the sequences and the grid divisible
+// by 8, the workgroups of XCD x take only the sequences x, x + 8, ..., so the resident blocks of an XCD are neighbours that
+// share most of their query tiles in the XCD's L2. A pre-pass (launch_backward_prepass) computes δ and zeroes dQ first.
+#include "attention_block_plan.hpp"
+#include "attention_device.hpp"
+#include "attention_launch.hpp"
+
+namespace rk {
+
+namespace {
+
+constexpr int kRing = 5;               // query tiles held at once: the four a step reads and the one loaded for the next
+constexpr int kTrStride = kTile + 4;   // transpose buffer row stride: conflict-free row writes and 128-bit row reads
+
+template<int D>
+struct BandShared {
+    float q[kRing][kSlotFloats<D>];            // Q tiles, row-major, rows D + 4 floats apart
+    float u[kRing][kSlotFloats<D>];            // dO tiles
+    float seed_s[kRing][kTile];                // per query: -(m·log2e + log2 l), or -inf where P = 0
+    float seed_d[kRing][kTile];                // per query: -δ
+    float dq[kRing][kSlotFloats<D>];           // dQ partial sums of the query tiles in flight, [query][feature]
+    float tr[kBlockTiles][kTile * kTrStride];  // per wave: dS transposed, [query][key]
+};
+
+// Quarter of a query tile (rows 8w .. 8w + 7) and the statistics of those rows, carried one step ahead.
+template<int D>
+struct BandQuarter {
+    f32x4 q[D / 32], u[D / 32];
+    float m, l, d;
+};
+
+template<int D>
+__global__ __launch_bounds__(kWave * kBlockTiles) void attention_band_backward_kernel(const Tensor q, const Tensor k,
+        const Tensor v, const uint8_t *__restrict__ mask, const float *__restrict__ lse, const Tensor du,
+        const float *__restrict__ delta, float *__restrict__ dq, float *__restrict__ dk, float *__restrict__ dv, const Shape s,
+        const int nblocks, const int groups, const float scale) {
+    constexpr int HALF = D / 2;
+    constexpr int DT = D / 32;
+    constexpr int S = kSlotStride<D>;
+    __shared__ __align__(16) BandShared<D> sh;
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave); // key tile of the block
+    const int col = lane & 31;
+    const int h = lane >> 5;
+    const float c2 = scale * kLog2e;
+    const int seqs = s.batch * s.heads;
+    const int qtiles = (s.queries + kTile - 1) / kTile;
+    const uint32_t kstep = 4u * k.st, vstep = 4u * v.st, qstep = 4u * q.st, ustep = 4u * du.st;
+
+    const int group = static_cast<int>(blockIdx.x) % groups;
+    const int member = static_cast<int>(blockIdx.x) / groups;
+    const int members = static_cast<int>(gridDim.x) / groups;
+    const int group_blocks = seqs / groups * nblocks;
+    for (int index = member; index < group_blocks; index += members) {
+        const int local_seq = index / nblocks;
+        const int kb = index - local_seq * nblocks;
+        const int seq = group + groups * local_seq;
+        const int b = seq / s.heads;
+        const int head = seq - b * s.heads;
+        const Buffer kbuf = make_buffer(sequence(k, b, head), sequence_bytes(s.keys, k.st, D));
+        const Buffer vbuf = make_buffer(sequence(v, b, head), sequence_bytes(s.keys, v.st, D));
+        const Buffer qbuf = make_buffer(sequence(q, b, head), sequence_bytes(s.queries, q.st, D));
+        const Buffer ubuf = make_buffer(sequence(du, b, head), sequence_bytes(s.queries, du.st, D));
+        const Buffer lbuf = make_buffer(lse + static_cast<int64_t>(seq) * s.queries * 2, static_cast<uint32_t>(s.queries) * 8u);
+        const Buffer dbuf = make_buffer(delta + static_cast<int64_t>(seq) * s.queries, static_cast<uint32_t>(s.queries) * 4u);
+        const Buffer mbuf = make_buffer(mask + static_cast<int64_t>(b) * s.keys, static_cast<uint32_t>(s.keys));
+        const Buffer qgbuf = make_buffer(dq + static_cast<int64_t>(seq) * s.queries * D, static_cast<uint32_t>(s.queries) * (4u * D));
+
+        // Bands of the block's four key tiles in whole query tiles [first, end) (empty past the last key), the skewed
+        // schedule (step i, wave w: query tile base + i + w) and the union of the bands.
+        int base = 0x7fffffff, stop = -0x7fffffff, union_lo = 0x7fffffff, union_hi = -0x7fffffff, my_first = 0, my_end = 0;
+        for (int x = 0; x < kBlockTiles; ++x) {
+            const int tile = kb * kBlockTiles + x;
+            int first = 0, last = 0;
+            if (tile * kTile >= s.keys || dkdv_query_range(s, tile, first, last) == 0) continue;
+            const int f = first / kTile, e = (last + kTile - 1) / kTile;
+            base = min(base, f - x);
+            stop = max(stop, e - x);
+            union_lo = min(union_lo, f);
+            union_hi = max(union_hi, e);
+            if (x == w) {
+                my_first = f;
+                my_end = e;
+            }
+        }
+        const int nsteps = stop > base ? stop - base : 0;
+
+        const int key0 = (kb * kBlockTiles + w) * kTile;
+        const int key = key0 + col;
+        const bool in_range = key < s.keys;
+        // Every load of the block is issued before the first wait (the mask byte too: keys past the end read 0 through
+        // kNoRow rather than a branch), so the block start costs one memory round trip.
+        const int mask_byte = buffer_load_byte(mbuf, in_range ? static_cast<uint32_t>(key) : kNoRow);
+
+        // K and V rows of this wave's key tile (row layout: B operands of S and dP), K pre-scaled by scale·log2e; K's
+        // column layout (A operand of dQᵀ), pre-scaled by 1/√D and zero for masked keys, whatever K holds there.
+        float kr[HALF], vr[HALF];
+        buffer_load_span<true>(kr, kbuf, in_range ? static_cast<uint32_t>(key) * kstep + 4u * h * HALF : kNoRow);
+        buffer_load_span<true>(vr, vbuf, in_range ? static_cast<uint32_t>(key) * vstep + 4u * h * HALF : kNoRow);
+        float kc[DT][16];
+        {
+            const uint32_t klane = static_cast<uint32_t>(key0 + 4 * h) * kstep + 4u * col;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+#pragma unroll
+                for (int t = 0; t < DT; ++t)
+                    kc[t][j] = buffer_load(kbuf, klane + 128u * t, static_cast<uint32_t>(8 * (j >> 2) + (j & 3)) * kstep);
+            }
+        }
+
+        // Query-tile quarters: rows 8w .. 8w + 7 of tile T, lane (row lane % 8, 16-byte chunk 8i + lane / 8), whole lines.
+        // Rows outside the sequence (T < 0 or past the end) read 0 and get P = 0.
+        auto load_quarter = [&](BandQuarter<D> &r, const int tile) __attribute__((always_inline)) {
+            const int query = tile * kTile + 8 * w + (lane & 7);
+            const bool ok = query >= 0 && query < s.queries; // kNoRow keeps the offset out of range for any stride
+            const uint32_t row = static_cast<uint32_t>(query);
+#pragma unroll
+            for (int i = 0; i < D / 32; ++i) {
+                const uint32_t chunk = static_cast<uint32_t>(8 * i + (lane >> 3));
+                r.q[i] = buffer_load4(qbuf, (ok ? row * qstep : kNoRow) + 16u * chunk, 0);
+                r.u[i] = buffer_load4(ubuf, (ok ? row * ustep : kNoRow) + 16u * chunk, 0);
+            }
+            r.m = buffer_load(lbuf, ok ? row * 8u : kNoRow, 0);
+            r.l = buffer_load(lbuf, ok ? row * 8u + 4u : kNoRow, 0);
+            r.d = buffer_load(dbuf, ok ? row * 4u : kNoRow, 0);
+        };
+        auto store_quarter = [&](const BandQuarter<D> &r, const int tile) __attribute__((always_inline)) {
+            const int slot = (tile + kRing) % kRing;
+            const int row = 8 * w + (lane & 7);
+#pragma unroll
+            for (int i = 0; i < D / 32; ++i) {
+                const int at = row * S + 4 * (8 * i + (lane >> 3));
+                *reinterpret_cast<f32x4 *>(&sh.q[slot][at]) = r.q[i];
+                *reinterpret_cast<f32x4 *>(&sh.u[slot][at]) = r.u[i];
+            }
+            const int query = tile * kTile + row;
+            const bool ok = query >= 0 && query < s.queries && r.m != -INFINITY;
+            // Straight-line arithmetic and a select: a branch here would let the compiler sink the statistic loads into
+            // it and wait for each of them in turn. l >= 1 for every row that sees a key (v_log_f32 needs no denormal care).
+            const float seed = -fmaf(r.m, kLog2e, __builtin_amdgcn_logf(r.l));
+            sh.seed_s[slot][row] = ok ? seed : -INFINITY; // P = exp2(S·scale·log2e + this)
+            sh.seed_d[slot][row] = -r.d;
+        };
+        // Adds query tile X's finished dQ slot into dQ (each wave a quarter: 8 rows, whole lines per instruction). Tiles
+        // outside the sequence, or that no wave of the block touched, hold zeros and are skipped.
+        auto flush = [&](const int tile) __attribute__((always_inline)) {
+            if (tile < 0 || tile >= qtiles || tile < union_lo || tile >= union_hi) return;
+            const float *slot = sh.dq[(tile + kRing) % kRing];
+            float x[D / 8];
+#pragma unroll
+            for (int r = 0; r < D / 8; ++r) {
+                const int e = r * kWave + lane;
+                x[r] = slot[(8 * w + e / D) * S + e % D];
+            }
+#pragma unroll
+            for (int r = 0; r < D / 8; ++r) {
+                const int e = r * kWave + lane;
+                const int row = 8 * w + e / D, feature = e % D;
+                const uint32_t voff = (static_cast<uint32_t>(tile * kTile + row) * D + static_cast<uint32_t>(feature)) * 4u;
+                __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(x[r], qgbuf, static_cast<int>(voff), 0, 0);
+            }
+        };
+
+        f32x16 acc_k[DT], acc_v[DT];
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+            acc_k[t] = f32x16{};
+            acc_v[t] = f32x16{};
+        }
+        BandQuarter<D> opening[kBlockTiles]; // the first four query tiles of the walk
+        if (nsteps > 0) {
+    #pragma unroll
+            for (int x = 0; x < kBlockTiles; ++x) load_quarter(opening[x], base + x);
+        }
+        const bool visible = mask_byte != 0;
+        const uint32_t bits = static_cast<uint32_t>(__ballot(visible));
+        if (bits == 0) my_end = my_first; // no visible key: the wave only keeps the schedule
+        const int qlo = window_query_lo(s, key);
+        const int qhi = min(window_query_hi(s, key), s.queries - 1);
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const bool kept = (bits >> tile_row(j, h)) & 1u;
+#pragma unroll
+            for (int t = 0; t < DT; ++t) kc[t][j] = kept ? kc[t][j] * scale : 0.0f;
+        }
+        if (nsteps > 0) { // a block that no query sees stores zero dK/dV below
+    #pragma unroll
+            for (int x = 0; x < kBlockTiles; ++x) store_quarter(opening[x], base + x);
+    #pragma unroll
+            for (int c = 0; c < HALF; ++c) kr[c] *= c2;
+            __syncthreads();
+
+            float *const tr = sh.tr[w];
+            for (int i = 0; i < nsteps; ++i) {
+                const int tile = base + i + w;
+                const int slot = (tile + kRing) % kRing;
+                const bool has_next = i + 1 < nsteps;
+                const bool first = w == kBlockTiles - 1 || i == 0; // no wave has given this query tile a share yet
+                float *const dslot = sh.dq[slot];
+                BandQuarter<D> next;
+                if (has_next) load_quarter(next, base + i + kBlockTiles);
+                if (tile < my_first || tile >= my_end) {
+                    if (first) {
+    #pragma unroll
+                        for (int t = 0; t < DT; ++t) {
+    #pragma unroll
+                            for (int j = 0; j < 16; ++j) dslot[tile_row(j, h) * S + 32 * t + col] = 0.0f;
+                        }
+                    }
+                } else {
+                    const int q0 = tile * kTile;
+                    // Each product's LDS reads are issued together, ahead of its MFMAs (sched_barrier keeps them there):
+                    // with one wave per SIMD nothing else covers an LDS round trip, so the wave waits once per operand
+                    // group instead of once per read. Accumulator register j holds query q0 + tile_row(j, h): the chains
+                    // start from its seeds.
+                    f32x16 sc, dp;
+                    {
+                        float qr[HALF];
+    #pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            const f32x4 a = *reinterpret_cast<const f32x4 *>(&sh.seed_s[slot][8 * u + 4 * h]);
+                            const f32x4 d = *reinterpret_cast<const f32x4 *>(&sh.seed_d[slot][8 * u + 4 * h]);
+    #pragma unroll
+                            for (int x = 0; x < 4; ++x) {
+                                sc[4 * u + x] = a[x];
+                                dp[4 * u + x] = d[x];
+                            }
+                        }
+                        read_row_layout<D>(sh.q[slot], qr);
+                        __builtin_amdgcn_sched_barrier(0);
+    #pragma unroll
+                        for (int c = 0; c < HALF; ++c) sc = mfma(qr[c], kr[c], sc);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                    {
+                        float ur[HALF];
+                        read_row_layout<D>(sh.u[slot], ur);
+                        __builtin_amdgcn_sched_barrier(0);
+    #pragma unroll
+                        for (int c = 0; c < HALF; ++c) dp = mfma(ur[c], vr[c], dp);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+    #pragma unroll
+                    for (int j = 0; j < 16; ++j) {
+                        const float p = exp2_fast(sc[j]);
+                        sc[j] = p;
+                        dp[j] *= p;
+                    }
+                    if (bits != 0xffffffffu || q0 + kTile > s.queries || !tile_in_window(s, q0, key0)) {
+                        const uint32_t keep = visible ? bit_range(qlo - q0, qhi - q0) >> (4 * h) : 0u;
+    #pragma unroll
+                        for (int j = 0; j < 16; ++j) {
+                            const bool ok = (keep >> (8 * (j >> 2) + (j & 3))) & 1u;
+                            sc[j] = ok ? sc[j] : 0.0f;
+                            dp[j] = ok ? dp[j] : 0.0f;
+                        }
+                    }
+                    // dS transposed through this wave's buffer: B operand of dQᵀ MFMA j is dS[query col][key tile_row(j, h)].
+                    wave_lds_sync();
+    #pragma unroll
+                    for (int j = 0; j < 16; ++j) tr[tile_row(j, h) * kTrStride + col] = dp[j];
+                    // dVᵀ += dOᵀ·P and dKᵀ += Qᵀ·dS, column layouts read from the staged tiles eight rows at a time, each
+                    // group read one group of MFMAs ahead of its use.
+                    auto products = [&](const float (&c)[DT][8], const f32x16 &bop, const int j0, f32x16 (&acc)[DT]) __attribute__((always_inline)) {
+    #pragma unroll
+                        for (int j = 0; j < 8; ++j) {
+    #pragma unroll
+                            for (int t = 0; t < DT; ++t) acc[t] = mfma(c[t][j], bop[j0 + j], acc[t]);
+                        }
+                    };
+                    {
+                        float ca[DT][8], cb[DT][8];
+                        read_column_layout<D, 0, 8>(sh.u[slot], ca);
+                        __builtin_amdgcn_sched_barrier(0);
+                        read_column_layout<D, 8, 8>(sh.u[slot], cb);
+                        __builtin_amdgcn_sched_barrier(0);
+                        products(ca, sc, 0, acc_v);
+                        __builtin_amdgcn_sched_barrier(0);
+                        read_column_layout<D, 0, 8>(sh.q[slot], ca);
+                        __builtin_amdgcn_sched_barrier(0);
+                        products(cb, sc, 8, acc_v);
+                        __builtin_amdgcn_sched_barrier(0);
+                        read_column_layout<D, 8, 8>(sh.q[slot], cb);
+                        __builtin_amdgcn_sched_barrier(0);
+                        products(ca, dp, 0, acc_k);
+                        __builtin_amdgcn_sched_barrier(0);
+                        products(cb, dp, 8, acc_k);
+                    }
+                    wave_lds_sync();
+                    // dQ share of this key tile, dS·K over its 32 keys (A = dS rows, B = K's column layout), chained onto the
+                    // query tile's partial sum: register j of slice t is query q0 + tile_row(j, h), feature 32t + col, so each
+                    // LDS access covers 32 consecutive features of two rows. The partial sum is read always and then
+                    // selected, so the reads are not branches.
+                    float bq[16];
+                    f32x16 acc_q[DT];
+    #pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const f32x4 x = *reinterpret_cast<const f32x4 *>(&tr[col * kTrStride + 8 * u + 4 * h]);
+                        bq[4 * u + 0] = x[0];
+                        bq[4 * u + 1] = x[1];
+                        bq[4 * u + 2] = x[2];
+                        bq[4 * u + 3] = x[3];
+                    }
+    #pragma unroll
+                    for (int t = 0; t < DT; ++t) {
+    #pragma unroll
+                        for (int j = 0; j < 16; ++j) acc_q[t][j] = dslot[tile_row(j, h) * S + 32 * t + col];
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+    #pragma unroll
+                    for (int t = 0; t < DT; ++t) {
+    #pragma unroll
+                        for (int j = 0; j < 16; ++j) acc_q[t][j] = first ? 0.0f : acc_q[t][j];
+    #pragma unroll
+                        for (int j = 0; j < 16; ++j) acc_q[t] = mfma(bq[j], kc[t][j], acc_q[t]);
+                    }
+    #pragma unroll
+                    for (int t = 0; t < DT; ++t) {
+    #pragma unroll
+                        for (int j = 0; j < 16; ++j) dslot[tile_row(j, h) * S + 32 * t + col] = acc_q[t][j];
+                    }
+                }
+                if (has_next) store_quarter(next, base + i + kBlockTiles);
+                __syncthreads(); // this step's dQ shares and the next step's tile are in LDS
+                flush(base + i); // wave 0 has just given query tile base + i its last share
+            }
+            // Query tiles still in flight after the walk: only waves 1..3 reached them.
+    #pragma unroll
+            for (int x = 0; x < kBlockTiles - 1; ++x) flush(base + nsteps + x);
+        }
+
+        // dK and dV of this wave's key tile (keys past the end fall outside the resources).
+        const Buffer kg = make_buffer(dk + static_cast<int64_t>(seq) * s.keys * D, static_cast<uint32_t>(s.keys) * (4u * D));
+        const Buffer vg = make_buffer(dv + static_cast<int64_t>(seq) * s.keys * D, static_cast<uint32_t>(s.keys) * (4u * D));
+        const uint32_t row = static_cast<uint32_t>(key) * (4u * D) + 16u * h;
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint32_t off = row + 128u * t + 32u * u; // features 32t + 8u + 4h .. +3
+                const f32x4 xk{acc_k[t][4 * u] * scale, acc_k[t][4 * u + 1] * scale, acc_k[t][4 * u + 2] * scale, acc_k[t][4 * u + 3] * scale};
+                const f32x4 xv{acc_v[t][4 * u], acc_v[t][4 * u + 1], acc_v[t][4 * u + 2], acc_v[t][4 * u + 3]};
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, xk), kg, static_cast<int>(off), 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, xv), vg, static_cast<int>(off), 0, 0);
+            }
+        }
+        __syncthreads(); // the next block overwrites both rings
+    }
+}
+
+Tensor tensor(const float *p, const rocmkernels_strides &st) { return Tensor{p, st.batch, st.head, st.token}; }
+
+template<int D>
+hipError_t launch(const BackwardArgs &a, const int cus, hipStream_t stream) {
+    const hipError_t error = launch_backward_prepass(D, a, stream);
+    if (error != hipSuccess) return error;
+    const Shape shape{a.batch, a.heads, a.queries, a.keys, a.radius, a.causal};
+    const float scale = 1.0f / sqrtf(static_cast<float>(D));
+    const int nblocks = (a.keys + kBlockKeys - 1) / kBlockKeys;
+    const long long seqs = static_cast<long long>(a.batch) * a.heads;
+    const long long blocks = seqs * nblocks;
+    int grid = static_cast<int>(blocks < cus ? blocks : cus);
+    const int groups = (seqs % 8 == 0 && grid % 8 == 0) ? 8 : 1;
+    hipLaunchKernelGGL((attention_band_backward_kernel<D>), dim3(static_cast<unsigned>(grid)), dim3(kWave * kBlockTiles), 0, stream,
+            tensor(a.q, a.qs), tensor(a.k, a.ks), tensor(a.v, a.vs), reinterpret_cast<const uint8_t *>(a.mask), a.lse,
+            tensor(a.upstream, a.us), a.delta, a.gradient_q, a.gradient_k, a.gradient_v, shape, nblocks, groups, scale);
+    return hipGetLastError();
+}
+
+} // namespace
+
+hipError_t launch_band_backward(const int D, const BackwardArgs &a, const int cus, hipStream_t stream) {
+    return D == 32 ? launch<32>(a, cus, stream) : launch<64>(a, cus, stream);
+}
+
+} // namespace rk

@@ -584,4 +584,21 @@ hipError_t launch_fused_backward(const int D, const BackwardArgs &a, const int c
     return D == 32 ? launch<32>(a, cus, stream) : launch<64>(a, cus, stream);
 }
 
+hipError_t launch_backward_prepass(const int D, const BackwardArgs &a, hipStream_t stream) {
+    const Shape shape{a.batch, a.heads, a.queries, a.keys, a.radius, a.causal};
+    const long long seqs = static_cast<long long>(a.batch) * a.heads;
+    const int64_t qrows = seqs * a.queries;
+    const int G = D / 4;
+    const int64_t threads = (2 * qrows > qrows * G) ? 2 * qrows : qrows * G; // dQ rows and delta; dK/dV are left alone
+    const unsigned grid = static_cast<unsigned>((threads + 255) / 256);
+    if (D == 32) {
+        hipLaunchKernelGGL((attention_fused_prepass_kernel<32>), dim3(grid), dim3(256), 0, stream, tensor(a.output, a.os),
+                tensor(a.upstream, a.us), a.delta, a.gradient_q, a.gradient_k, a.gradient_v, shape, qrows, int64_t{0}, 0x7fffffff);
+    } else {
+        hipLaunchKernelGGL((attention_fused_prepass_kernel<64>), dim3(grid), dim3(256), 0, stream, tensor(a.output, a.os),
+                tensor(a.upstream, a.us), a.delta, a.gradient_q, a.gradient_k, a.gradient_v, shape, qrows, int64_t{0}, 0x7fffffff);
+    }
+    return hipGetLastError();
+}
+
 } // namespace rk

@@ -112,4 +112,11 @@ hipError_t launch_backward(int D, BackwardStage stage, const BackwardArgs &a, hi
 // (every pointer 16-byte aligned, every stride a multiple of 4); called by launch_backward for kBackwardFused.
 hipError_t launch_fused_backward(int D, const BackwardArgs &a, int cus, hipStream_t stream);
 
+// The fused backward's pre-pass alone: delta = sum(dO * O) per query row and dQ = 0 (dK/dV untouched).
+hipError_t launch_backward_prepass(int D, const BackwardArgs &a, hipStream_t stream);
+
+// Fused backward for radius windows (attention_backward_band.hip), D = 32 or 64 with 128-bit access: runs the pre-pass,
+// then one persistent workgroup per CU over whole 128-key blocks with skewed query tiles.
+hipError_t launch_band_backward(int D, const BackwardArgs &a, int cus, hipStream_t stream);
+
 } // namespace rk

@@ -392,6 +392,10 @@ def run_fused_and_default(device, q, k, v, du, mask, radius, causal):
     (32, 2, 4, 64, 64, -1, True, False),
     (64, 2, 4, 100, 100, 9, True, True),    # radius and padding at d=64
     (32, 1, 2, 40, 200, 5, False, False),   # key tiles past query 45 see no query: their dK/dV are zero
+    (64, 1, 2, 300, 300, 40, False, True),  # radius windows: a band on both sides of the diagonal
+    (64, 2, 1, 150, 150, 500, True, False), # a radius wider than the sequence
+    (32, 2, 2, 77, 300, 30, False, True),   # more keys than queries: most key tiles' bands are empty
+    (64, 1, 1, 300, 77, 30, True, False),   # more queries than keys: the band walk runs past the last key block
 ])
 def test_fused_backward_matches_oracle(device, width, batch, heads, queries, keys, radius, causal, pad):
     q, k, v, du = normal_case(700 + queries + keys, width, batch, heads, queries, keys)
@@ -455,8 +459,9 @@ def test_fused_backward_config3_and_masked_batch(device):
 @pytest.mark.parametrize("width,batch,length,radius", [(32, 64, 2048, -1), (64, 32, 4096, -1), (64, 16, 8192, 256)])
 def test_fused_backward_dispatch_order_subset(device, width, batch, length, radius):
     # 64 x 2048 causal at d=32 and 32 x 4096 at d=64: more key blocks (1024) than the piece table holds, so one workgroup
-    # per whole block in dispatch order, every dK/dV stored. Config 5 (radius 256): the fused flag runs the deterministic
-    # kernels. Checked on two sequences against the oracle, and the whole batch against the deterministic backward.
+    # per whole block in dispatch order, every dK/dV stored. Config 5 (radius 256): the band kernel, one workgroup per CU
+    # over whole key blocks. Checked on two sequences against the oracle, and the whole batch against the deterministic
+    # backward.
     q, k, v, du = normal_case(960 + width, width, batch, 1, length, length)
     mask = np.ones((batch, length), np.uint8)
     mask[1, length // 3:] = 0
