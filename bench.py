@@ -319,12 +319,14 @@ def load_traffic(kernel, config):
 
 def backward_traffic(config, part):
     """HBM and algorithmic bytes per launch of the kernels one backward call runs, from profiles/traffic.json: the fused
-    pre-pass and kernel for the default backward where the library takes it (no radius window), the dQ and dK/dV
-    kernels otherwise and for the deterministic backward."""
+    pre-pass and the fused (no radius window) or band kernel for the default backward where the library takes them
+    (128-bit access, which the bench inputs have, and no radius window at d=32: rk::run in attention_backward.hip), the
+    dQ and dK/dV kernels otherwise and for the deterministic backward."""
     suffix = f" config{profile_config(config)}"
     rows = {k[:-len(suffix)]: v for k, v in traffic_table().items() if k.endswith(suffix) and "forward_kernel" not in k}
-    fused = part == "backward" and CONFIGS[config]["radius"] < 0
-    names = sorted(n for n in rows if ("fused" in n) == fused)
+    cfg = CONFIGS[config]
+    fused = part == "backward" and (cfg["radius"] < 0 or cfg["width"] == 64)
+    names = sorted(n for n in rows if ("fused" in n or "band" in n) == fused)
     if not names:
         return None
     return {"kernels": names, "hbm_bytes_per_launch": sum(rows[n]["hbm_bytes_per_launch"] for n in names),
