@@ -17,10 +17,11 @@
 // (Attention.hip:211-221). Streamed operands are read through buffer resources (see attention_device.hpp), and
 // each tile's row-layout operands are loaded one tile ahead, after the current tile's MFMAs are issued.
 //
-// Fused variant (opt-in, flag ROCMKERNELS_ATTENTION_FUSED_BACKWARD): kernel 1 only computes δ and zeroes dQ;
+// Per-key-tile fused variant (the fused flag's choice for inputs without 128-bit access; with it the key-block kernels
+// of attention_backward_fused.hip and attention_backward_band.hip run): kernel 1 only computes δ and zeroes dQ;
 // kernel 2 also forms dQ = dS·K/√D for each tile it visits and adds it into dQ with FP32 atomics. That is 5
 // GEMMs per visited tile instead of 7 (kernel 1 no longer recomputes S and dP), at the price of a dQ whose
-// low bits depend on the order in which the atomics land.
+// low bits depend on the order in which the atomics land. run<D, VEC> at the end of this file picks the path.
 #include "attention_device.hpp"
 #include "attention_launch.hpp"
 
@@ -815,8 +816,8 @@ hipError_t run(BackwardStage stage, const BackwardArgs &a, const int cus, hipStr
     const int64_t kitems = static_cast<int64_t>((a.keys + kTile - 1) / kTile) * a.batch * a.heads;
     // The fused key-block kernels need 128-bit access; without it the deterministic kernels measured faster.
     // Auto takes the fused kernels wherever they exist (128-bit access) and measured faster: under a radius window at
-    // D = 32 the band kernel did not (16 sequences x 8192 tokens, radius 256, causal: 149 us against 146 us for the
-    // deterministic pair; at D = 64 276 us against 287 us).
+    // D = 32 the band kernel did not (16 sequences x 8192 tokens, radius 256, causal: 147 us against 146 us for the
+    // deterministic pair; at D = 64 277 us against 288 us).
     if (stage == kBackwardAuto) stage = VEC && (a.radius < 0 || D == 64) ? kBackwardFused : kBackwardAll;
     if (stage == kBackwardFused) {
         // Key-block kernels (one dQ add per element per 128 keys): without a radius window the piece-planned one; under a

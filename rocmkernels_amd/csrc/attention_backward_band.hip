@@ -18,12 +18,11 @@
 // in LDS (queries onto lanes), K's column layout is held in registers (pre-scaled by 1/√D, zero for masked keys). The
 // share is summed in the query tile's slot of a second ring of five LDS tiles. Within a step the four waves work on four
 // different query tiles, and query tile T meets wave 3, 2, 1 and 0 in four consecutive steps, so the sum needs no atomics
-// (LDS float atomics cost several times the step's MFMAs): the first wave to reach the tile (wave 3, or any wave at the
-// walk's first step, since the earlier waves' bands cannot hold it) stores its share, zero when its key tile does not see
-// the query tile, and each later wave loads the partial sum as the start of its dQ chain and stores the result. The last
-// contribution comes from wave 0 at step (tile - base); after that step's barrier the four waves add the slot to dQ with
-// FP32 buffer atomics (one add per dQ element per key block, as in the key-block kernel). Blocks are never split: dK
-// and dV are stored once.
+// (LDS float atomics cost several times the step's MFMAs): each wave that sees the tile loads the partial sum as the
+// start of its dQ chain and stores the result. The last contribution comes from wave 0 at step (tile - base); after that
+// step's barrier the four waves add the slot to dQ with FP32 buffer atomics (one add per dQ element per key block, as in
+// the key-block kernel) and zero it, so the ring is zero wherever a walk starts a tile (it is cleared once at the start).
+// Blocks are never split: dK and dV are stored once.
 //
 // Work mapping: one persistent workgroup per CU walks the blocks g, g + G, ...; with the sequences and the grid divisible
 // by 8, the workgroups of XCD x take only the sequences x, x + 8, ..., so the resident blocks of an XCD are neighbours that
@@ -75,6 +74,9 @@ __global__ __launch_bounds__(kWave * kBlockTiles) void attention_band_backward_k
     const int qtiles = (s.queries + kTile - 1) / kTile;
     const uint32_t kstep = 4u * k.st, vstep = 4u * v.st, qstep = 4u * q.st, ustep = 4u * du.st;
 
+    // The dQ ring starts at zero; every flush zeroes the slot it empties (the first block's barrier orders these stores).
+    for (int e = 4 * static_cast<int>(threadIdx.x); e < kRing * kSlotFloats<D>; e += 4 * kWave * kBlockTiles)
+        *reinterpret_cast<f32x4 *>(&sh.dq[0][0] + e) = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const int group = static_cast<int>(blockIdx.x) % groups;
     const int member = static_cast<int>(blockIdx.x) / groups;
     const int members = static_cast<int>(gridDim.x) / groups;
@@ -169,16 +171,17 @@ __global__ __launch_bounds__(kWave * kBlockTiles) void attention_band_backward_k
             sh.seed_s[slot][row] = ok ? seed : -INFINITY; // P = exp2(S·scale·log2e + this)
             sh.seed_d[slot][row] = -r.d;
         };
-        // Adds query tile X's finished dQ slot into dQ (each wave a quarter: 8 rows, whole lines per instruction). Tiles
-        // outside the sequence, or that no wave of the block touched, hold zeros and are skipped.
+        // Adds query tile X's finished dQ slot into dQ (each wave a quarter: 8 rows, whole lines per instruction) and
+        // zeroes it. Tiles outside the sequence, or that no wave of the block touched, hold zeros and are skipped.
         auto flush = [&](const int tile) __attribute__((always_inline)) {
             if (tile < 0 || tile >= qtiles || tile < union_lo || tile >= union_hi) return;
-            const float *slot = sh.dq[(tile + kRing) % kRing];
+            float *slot = sh.dq[(tile + kRing) % kRing];
             float x[D / 8];
 #pragma unroll
             for (int r = 0; r < D / 8; ++r) {
                 const int e = r * kWave + lane;
                 x[r] = slot[(8 * w + e / D) * S + e % D];
+                slot[(8 * w + e / D) * S + e % D] = 0.0f;
             }
 #pragma unroll
             for (int r = 0; r < D / 8; ++r) {
@@ -223,19 +226,10 @@ __global__ __launch_bounds__(kWave * kBlockTiles) void attention_band_backward_k
                 const int tile = base + i + w;
                 const int slot = (tile + kRing) % kRing;
                 const bool has_next = i + 1 < nsteps;
-                const bool first = w == kBlockTiles - 1 || i == 0; // no wave has given this query tile a share yet
                 float *const dslot = sh.dq[slot];
                 BandQuarter<D> next;
                 if (has_next) load_quarter(next, base + i + kBlockTiles);
-                if (tile < my_first || tile >= my_end) {
-                    if (first) {
-    #pragma unroll
-                        for (int t = 0; t < DT; ++t) {
-    #pragma unroll
-                            for (int j = 0; j < 16; ++j) dslot[tile_row(j, h) * S + 32 * t + col] = 0.0f;
-                        }
-                    }
-                } else {
+                if (tile >= my_first && tile < my_end) {
                     const int q0 = tile * kTile;
                     // Each product's LDS reads are issued together, ahead of its MFMAs (sched_barrier keeps them there):
                     // with one wave per SIMD nothing else covers an LDS round trip, so the wave waits once per operand
@@ -317,8 +311,7 @@ __global__ __launch_bounds__(kWave * kBlockTiles) void attention_band_backward_k
                     wave_lds_sync();
                     // dQ share of this key tile, dS·K over its 32 keys (A = dS rows, B = K's column layout), chained onto the
                     // query tile's partial sum: register j of slice t is query q0 + tile_row(j, h), feature 32t + col, so each
-                    // LDS access covers 32 consecutive features of two rows. The partial sum is read always and then
-                    // selected, so the reads are not branches.
+                    // LDS access covers 32 consecutive features of two rows.
                     float bq[16];
                     f32x16 acc_q[DT];
     #pragma unroll
@@ -337,8 +330,6 @@ __global__ __launch_bounds__(kWave * kBlockTiles) void attention_band_backward_k
                     __builtin_amdgcn_sched_barrier(0);
     #pragma unroll
                     for (int t = 0; t < DT; ++t) {
-    #pragma unroll
-                        for (int j = 0; j < 16; ++j) acc_q[t][j] = first ? 0.0f : acc_q[t][j];
     #pragma unroll
                         for (int j = 0; j < 16; ++j) acc_q[t] = mfma(bq[j], kc[t][j], acc_q[t]);
                     }
