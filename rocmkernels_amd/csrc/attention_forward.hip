@@ -216,15 +216,25 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
     }
     const float mc_run = mc; // offset the wave's (l_run, o) are expressed against
 
-    // Merge the states of the `split` waves of the item: waves with sub > 0 publish (m, l, mc, Oᵀ) in LDS, the
-    // wave with sub == 0 combines. Every state satisfies l_w = Σ exp2(s·c2 - mc_w); they are combined against the
-    // largest offset, and lse's sum is then expressed against the true maximum.
+    // Merge the states of the `split` waves of the item. Every state satisfies l_w = Σ exp2(s·c2 - mc_w); they are
+    // combined against the largest offset, and lse's sum is then expressed against the true maximum. The sum runs in
+    // the same order whichever wave computes it (state 0 scaled, then states 1 .. SPLIT - 1 added).
+    //   * Dispatch order (NI = 0): waves with sub > 0 publish (m, l, mc, Oᵀ) in LDS and the wave with sub == 0
+    //     combines and stores everything; other workgroups keep the CU busy meanwhile.
+    //   * Persistent bins (NI > 0): the item's end is on the CU's critical path, so every wave publishes its state and
+    //     after the barrier each merges and stores its own share of the output registers (NREG / SPLIT of them, whole
+    //     16-byte row chunks): config 2 forward 19.04 -> 18.9 us (the last item's merge and store end sooner). In
+    //     dispatch order the extra LDS traffic made configs 4 and 5 2-2.5% slower.
+    constexpr int SHARERS = NI > 0 ? SPLIT : 1; // waves that finalise the item's output
+    constexpr int NR = NREG / SHARERS;          // output registers each of them finalises
     float m_all = m_run;
     float mc_all = mc_run;
     float base = 0.0f, l_all = l_run;
+    float share[SHARERS > 1 && NR > 0 ? NR : 1];
+    const int r0 = sub * NR; // first of them (register j of slice t is 16t + j)
     if constexpr (SPLIT > 1) {
         __shared__ float partial[WG][NREG + 3][kWave];
-        if (sub > 0) {
+        if (SHARERS > 1 || sub > 0) {
             partial[wave][0][lane] = m_run;
             partial[wave][1][lane] = l_run;
             partial[wave][2 + NREG][lane] = mc_run;
@@ -237,28 +247,55 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
             }
         }
         __syncthreads();
-        if (sub != 0) return;
+        if (sub >= SHARERS) return;
+        if constexpr (SHARERS > 1) {
+            const int w0 = wave - sub; // the item's first wave
+            m_all = partial[w0][0][lane];
+            mc_all = partial[w0][2 + NREG][lane];
 #pragma unroll
-        for (int x = 1; x < split; ++x) {
-            m_all = fmaxf(m_all, partial[wave + x][0][lane]);
-            mc_all = fmaxf(mc_all, partial[wave + x][2 + NREG][lane]);
-        }
-        base = mc_all == -INFINITY ? 0.0f : mc_all;
-        const float a0 = exp2_fast(mc_run - base);
-        l_all = l_run * a0;
-        if constexpr (!STATS) {
+            for (int x = 1; x < split; ++x) {
+                m_all = fmaxf(m_all, partial[w0 + x][0][lane]);
+                mc_all = fmaxf(mc_all, partial[w0 + x][2 + NREG][lane]);
+            }
+            base = mc_all == -INFINITY ? 0.0f : mc_all;
+            float a[SPLIT];
 #pragma unroll
-            for (int t = 0; t < DT; ++t) o[t] *= a0;
-        }
+            for (int x = 0; x < split; ++x) a[x] = exp2_fast(partial[w0 + x][2 + NREG][lane] - base);
+            l_all = partial[w0][1][lane] * a[0];
 #pragma unroll
-        for (int x = 1; x < split; ++x) {
-            const float aw = exp2_fast(partial[wave + x][2 + NREG][lane] - base);
-            l_all = fmaf(partial[wave + x][1][lane], aw, l_all);
+            for (int x = 1; x < split; ++x) l_all = fmaf(partial[w0 + x][1][lane], a[x], l_all);
             if constexpr (!STATS) {
 #pragma unroll
-                for (int t = 0; t < DT; ++t) {
+                for (int k = 0; k < NR; ++k) {
+                    float acc = partial[w0][2 + r0 + k][lane] * a[0];
 #pragma unroll
-                    for (int j = 0; j < 16; ++j) o[t][j] = fmaf(partial[wave + x][2 + 16 * t + j][lane], aw, o[t][j]);
+                    for (int x = 1; x < split; ++x) acc = fmaf(partial[w0 + x][2 + r0 + k][lane], a[x], acc);
+                    share[k] = acc;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int x = 1; x < split; ++x) {
+                m_all = fmaxf(m_all, partial[wave + x][0][lane]);
+                mc_all = fmaxf(mc_all, partial[wave + x][2 + NREG][lane]);
+            }
+            base = mc_all == -INFINITY ? 0.0f : mc_all;
+            const float a0 = exp2_fast(mc_run - base);
+            l_all = l_run * a0;
+            if constexpr (!STATS) {
+#pragma unroll
+                for (int t = 0; t < DT; ++t) o[t] *= a0;
+            }
+#pragma unroll
+            for (int x = 1; x < split; ++x) {
+                const float aw = exp2_fast(partial[wave + x][2 + NREG][lane] - base);
+                l_all = fmaf(partial[wave + x][1][lane], aw, l_all);
+                if constexpr (!STATS) {
+#pragma unroll
+                    for (int t = 0; t < DT; ++t) {
+#pragma unroll
+                        for (int j = 0; j < 16; ++j) o[t][j] = fmaf(partial[wave + x][2 + 16 * t + j][lane], aw, o[t][j]);
+                    }
                 }
             }
         }
@@ -275,17 +312,39 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
     if constexpr (!STATS) {
         const float factor = has_keys ? 1.0f / l_all : (nan_row ? NAN : 0.0f);
         float *orow = out + static_cast<int64_t>(b) * osb + static_cast<int64_t>(head) * osh + static_cast<int64_t>(query) * ost;
+        if constexpr (SHARERS == 1) {
 #pragma unroll
-        for (int t = 0; t < DT; ++t) {
-            if (has_keys) {
-                store_tile_row<VEC, ROWS>(orow + 32 * t, o[t], factor, h);
-            } else {
-                const f32x16 fill{};
-                store_tile_row<VEC, ROWS>(orow + 32 * t, fill + factor, 1.0f, h);
+            for (int t = 0; t < DT; ++t) {
+                if (has_keys) {
+                    store_tile_row<VEC, ROWS>(orow + 32 * t, o[t], factor, h);
+                } else {
+                    const f32x16 fill{};
+                    store_tile_row<VEC, ROWS>(orow + 32 * t, fill + factor, 1.0f, h);
+                }
+            }
+        } else {
+            // Registers 16t + 4u .. +3 are features 32t + 8u + 4h .. +3 of this lane's query; a 16-wide head stores only
+            // its first two chunks (u < 2).
+#pragma unroll
+            for (int q4 = 0; q4 < NR / 4; ++q4) {
+                const int r = r0 + 4 * q4, t = r >> 4, u = (r & 15) >> 2;
+                if (u >= ROWS / 8) continue;
+                const f32x4 x = has_keys ? f32x4{share[4 * q4] * factor, share[4 * q4 + 1] * factor, share[4 * q4 + 2] * factor,
+                                                 share[4 * q4 + 3] * factor}
+                                         : f32x4{factor, factor, factor, factor};
+                float *dst = orow + 32 * t + 8 * u + 4 * h;
+                if constexpr (VEC) {
+                    *reinterpret_cast<f32x4 *>(dst) = x;
+                } else {
+                    dst[0] = x[0];
+                    dst[1] = x[1];
+                    dst[2] = x[2];
+                    dst[3] = x[3];
+                }
             }
         }
     }
-    if (h == 0) {
+    if (h == 0 && sub == 0) {
         const int64_t row = static_cast<int64_t>(seq) * s.queries + query;
         lse[2 * row] = has_keys ? m_all * scale : (nan_row ? NAN : -INFINITY);
         lse[2 * row + 1] = has_keys ? sum_at_max : (nan_row ? NAN : 0.0f);
