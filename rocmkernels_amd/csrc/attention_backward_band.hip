@@ -96,24 +96,11 @@ __global__ __launch_bounds__(kWave * kBlockTiles) void attention_band_backward_k
         const Buffer mbuf = make_buffer(mask + static_cast<int64_t>(b) * s.keys, static_cast<uint32_t>(s.keys));
         const Buffer qgbuf = make_buffer(dq + static_cast<int64_t>(seq) * s.queries * D, static_cast<uint32_t>(s.queries) * (4u * D));
 
-        // Bands of the block's four key tiles in whole query tiles [first, end) (empty past the last key), the skewed
-        // schedule (step i, wave w: query tile base + i + w) and the union of the bands.
-        int base = 0x7fffffff, stop = -0x7fffffff, union_lo = 0x7fffffff, union_hi = -0x7fffffff, my_first = 0, my_end = 0;
-        for (int x = 0; x < kBlockTiles; ++x) {
-            const int tile = kb * kBlockTiles + x;
-            int first = 0, last = 0;
-            if (tile * kTile >= s.keys || dkdv_query_range(s, tile, first, last) == 0) continue;
-            const int f = first / kTile, e = (last + kTile - 1) / kTile;
-            base = min(base, f - x);
-            stop = max(stop, e - x);
-            union_lo = min(union_lo, f);
-            union_hi = max(union_hi, e);
-            if (x == w) {
-                my_first = f;
-                my_end = e;
-            }
-        }
-        const int nsteps = stop > base ? stop - base : 0;
+        // The skewed schedule (step i, wave w: query tile base + i + w), this wave's band and the union of the bands.
+        const BandWalk walk = band_walk(s.queries, s.keys, s.radius, s.causal, kb);
+        const int base = walk.base, nsteps = walk.nsteps, union_lo = walk.lo, union_hi = walk.hi;
+        int my_first, my_end;
+        key_tile_band(s.queries, s.keys, s.radius, s.causal, kb * kBlockTiles + w, my_first, my_end);
 
         const int key0 = (kb * kBlockTiles + w) * kTile;
         const int key = key0 + col;

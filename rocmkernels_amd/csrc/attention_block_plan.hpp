@@ -43,6 +43,65 @@ __host__ __device__ inline int block_query_tiles(const int queries, const int ke
     return last > first ? (last + 31) / 32 - first_tile : 0;
 }
 
+// ---- band walk (attention_backward_band.hip) ------------------------------------------------------------------
+// Under a radius window each 32-key tile sees a band of query tiles, one tile later for each key tile. The band kernel
+// walks a key block skewed: at step i the wave of key tile x works on query tile base + i + x, so each wave meets the
+// tiles of its own band in order and no two waves share a tile within a step.
+
+// Queries [first, last) that can see some key of 32-key tile kt through the causal and radius windows (the keys'
+// padding mask aside); returns the number of 32-query tiles they span.
+__host__ __device__ inline int key_tile_queries(const int queries, const int radius, const int causal, const int kt, int &first,
+        int &last) {
+    const int key0 = kt * 32;
+    first = causal ? key0 : 0;
+    last = queries;
+    if (radius >= 0) {
+        first = key0 - radius > first ? key0 - radius : first;
+        last = key0 + 32 + radius < last ? key0 + 32 + radius : last;
+    }
+    first = first > 0 ? first : 0;
+    return last > first ? (last - first + 31) / 32 : 0;
+}
+
+// Band of 32-key tile kt in whole query tiles [first, end): empty (first == end == 0) when the tile starts past the
+// sequence's last key or no query sees it.
+__host__ __device__ inline void key_tile_band(const int queries, const int keys, const int radius, const int causal, const int kt,
+        int &first, int &end) {
+    int q0 = 0, q1 = 0;
+    if (kt * 32 < keys && key_tile_queries(queries, radius, causal, kt, q0, q1) > 0) {
+        first = q0 / 32;
+        end = (q1 + 31) / 32;
+    } else {
+        first = end = 0;
+    }
+}
+
+struct BandWalk {
+    int base = 0x7fffffff;      // query tile of the block's first key tile at step 0
+    int nsteps = 0;             // steps of the walk (0: no query sees the block)
+    int lo = 0x7fffffff;        // query tiles [lo, hi) of the union of the four bands
+    int hi = -0x7fffffff;
+};
+
+// The walk of key block kb: base = min over the block's key tiles x of (band start - x), so that at step 0 no wave is
+// past its band's start, and nsteps reaches the latest (band end - x).
+__host__ __device__ inline BandWalk band_walk(const int queries, const int keys, const int radius, const int causal,
+        const int kb) {
+    BandWalk b;
+    int stop = -0x7fffffff;
+    for (int x = 0; x < kBlockTiles; ++x) {
+        int f = 0, e = 0;
+        key_tile_band(queries, keys, radius, causal, kb * kBlockTiles + x, f, e);
+        if (e <= f) continue;
+        b.base = b.base < f - x ? b.base : f - x;
+        stop = stop > e - x ? stop : e - x;
+        b.lo = b.lo < f ? b.lo : f;
+        b.hi = b.hi > e ? b.hi : e;
+    }
+    b.nsteps = stop > b.base ? stop - b.base : 0;
+    return b;
+}
+
 // ---- piece table ---------------------------------------------------------------------------------------------
 // Entry g * slots + j of the table (passed by value in the kernel arguments) is the j-th piece of workgroup g:
 // block index (sequence * blocks per sequence + kb) in bits 0-15, first query tile of the piece relative to the

@@ -19,6 +19,7 @@
 
 #include <stdint.h>
 
+#include "attention_block_plan.hpp"
 #include "attention_plan.hpp"
 
 namespace rk {
@@ -275,15 +276,7 @@ __host__ __device__ inline int forward_key_range(const Shape &s, const int qt, i
 // Queries [first, last) that can see some key of key tile kt through the causal and radius windows; returns the
 // number of 32-query tiles they span (the work of one dK/dV item when any of its keys is unmasked).
 __host__ __device__ inline int dkdv_query_range(const Shape &s, const int kt, int &first, int &last) {
-    const int key0 = kt * kTile;
-    first = s.causal ? key0 : 0;
-    last = s.queries;
-    if (s.radius >= 0) {
-        first = key0 - s.radius > first ? key0 - s.radius : first;
-        last = key0 + kTile + s.radius < last ? key0 + kTile + s.radius : last;
-    }
-    first = first > 0 ? first : 0;
-    return last > first ? (last - first + kTile - 1) / kTile : 0;
+    return key_tile_queries(s.queries, s.radius, s.causal, kt, first, last);
 }
 
 __host__ __device__ inline int forward_item_tiles(const Shape &s, const int qt) {

@@ -155,6 +155,17 @@ def test_fused_backward_block_plan_covers_every_tile_once_and_balances(tmp_path)
     assert "0 failure(s)" in result.stdout
 
 
+def test_band_backward_walk_covers_every_band_and_hands_dq_over_safely(tmp_path):
+    binary = str(tmp_path / "band_walk_check")
+    source = os.path.join(ROOT, "tests", "cpp", "band_walk_check.cpp")
+    csrc = os.path.join(ROOT, "rocmkernels_amd", "csrc")
+    subprocess.run(["g++", "-std=c++17", "-O1", "-Wall", "-Wextra", "-Werror", "-D__HIP_PLATFORM_AMD__", f"-I{csrc}",
+                    "-I/opt/rocm/include", source, "-o", binary], check=True, capture_output=True, text=True)
+    result = subprocess.run([binary], capture_output=True, text=True, timeout=120)
+    assert result.returncode == 0, result.stdout + result.stderr
+    assert "0 failure(s)" in result.stdout
+
+
 def test_autograd_binding_rejects_host_tensors():
     import torch
 
