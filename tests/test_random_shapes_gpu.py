@@ -15,6 +15,7 @@ pytestmark = pytest.mark.gpu
 
 CASES = 48
 GENERIC_CASES = 24
+BAND_CASES = 24
 
 
 def draw(seed, widths):
@@ -94,3 +95,29 @@ def test_random_generic_fp32_case_matches_oracle(device, seed):
     out, lse = attention.generic_forward(tq, tk, tv, tm, radius=case["radius"], output=out)
     out, lse = host(out, lse)
     check_forward(out, lse, want, label)
+
+
+@pytest.mark.parametrize("seed", range(BAND_CASES))
+def test_random_band_case_matches_oracle(device, seed):
+    # Radius windows with 128-bit access (packed or token-major views): the band backward kernel under the fused flag
+    # (both widths) and the default (width 64); lengths up to 700, so blocks walk several query tiles, with partial last
+    # key blocks, Lq != Lk, padding that can empty a batch, and windows from 0 to wider than the sequence.
+    rng = np.random.default_rng(7000 + seed)
+    queries = int(rng.integers(1, 701))
+    keys = queries if rng.random() < 0.5 else int(rng.integers(1, 701))
+    case = dict(width=int(rng.choice([32, 64])), batch=int(rng.integers(1, 3)), heads=int(rng.integers(1, 3)), queries=queries,
+                keys=keys, causal=bool(rng.random() < 0.6), radius=int(rng.choice([0, 1, 31, 32, int(rng.integers(0, 300)), 800])),
+                lengths=[int(x) for x in rng.integers(0, keys + 1, size=2)] if rng.random() < 0.4 else None,
+                layout=str(rng.choice(["packed", "token_major"])), fused=bool(rng.random() < 0.5))
+    label = f"band seed {seed}: {case}"
+    q, k, v, du = normal_case(8000 + 10 * seed, case["width"], case["batch"], case["heads"], case["queries"], case["keys"])
+    mask = key_mask(case)
+    want = oracle.attention(q, k, v, mask, du, radius=case["radius"], causal=case["causal"])
+    tq, tk, tv, tdu = (place(device, a, case["layout"]) for a in (q, k, v, du))
+    tm = torch.from_numpy(mask).to(device)
+    out, lse = attention.forward(tq, tk, tv, tm, radius=case["radius"], causal=case["causal"], entry="flash")
+    gq, gk, gv, delta = attention.backward(tq, tk, tv, tm, out, lse, tdu, radius=case["radius"], causal=case["causal"],
+                                           entry="ex", fused=case["fused"])
+    out, lse, gq, gk, gv, delta = host(out, lse, gq, gk, gv, delta)
+    check_forward(out, lse, want, label)
+    check_backward(gq, gk, gv, delta, want, label)
