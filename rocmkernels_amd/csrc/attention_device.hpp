@@ -435,11 +435,12 @@ __device__ __forceinline__ void split_sum(f32x16 (&acc)[N], const int sub) {
 }
 
 // True when every (query, key) pair of the 32x32 tile at (q0, key0) is inside the causal/radius window.
+// Written as integer limits and two comparisons so that the test stays in scalar instructions (branchy boolean
+// logic was lowered to lane masks and VALU selects, five VALU operations per tile).
 __device__ __forceinline__ bool tile_in_window(const Shape &s, const int q0, const int key0) {
-    bool ok = true;
-    if (s.causal) ok = ok && key0 + kTile - 1 <= q0;
-    if (s.radius >= 0) ok = ok && q0 + kTile - 1 - key0 <= s.radius && key0 + kTile - 1 - q0 <= s.radius;
-    return ok;
+    const int reach = s.radius >= 0 ? s.radius : 0x40000000; // largest |query - key| allowed
+    const int ahead = min(reach, s.causal ? 0 : 0x40000000);  // largest key - query allowed
+    return key0 + kTile - 1 - q0 <= ahead && q0 + kTile - 1 - key0 <= reach;
 }
 
 } // namespace rk

@@ -80,16 +80,22 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
     if constexpr (VEC) load_row_tile<D>(qraw, qbuf, 4u * q.st, static_cast<uint32_t>(q0) * (4u * q.st)); // rows >= queries read 0
     else buffer_load_span<VEC>(qr, qbuf, static_cast<uint32_t>(query) * (4u * q.st) + 4u * h * HALF);
 
-    // Online-softmax state of this lane's query over the tiles this wave visits. m_run is the raw maximum of q·k.
+    // Online-softmax state of this lane's query over the tiles this wave visits. m_half is the raw maximum of q·k
+    // over the keys this half-wave holds (16 of each tile); the row maximum is the larger of the two halves', formed
+    // only when it is needed (a re-base, and once at the end), so a tile costs no cross-half exchange.
     // The exponentials are taken against a reference offset mc (in log2 units, c2-scaled): p = exp2(s·c2 - mc).
     // mc moves only when the running maximum exceeds it by more than kLazy (so p <= 2^kLazy, far from overflow);
-    // o and l are then rescaled by exp2(mc_old - mc_new). The lse sum is brought to the true maximum once at
-    // the end. Skipping most rescales removes 16·D/32 VALU multiplies per tile, which matters because FP32 MFMA
-    // and VALU share the SIMD on gfx950: every VALU cycle adds to the MFMA time.
+    // o and l are then rescaled by exp2(mc_old - mc_new). The test compares raw maxima with m_lazy, the raw
+    // score at which p would reach 2^kLazy: a row's maximum exceeds it exactly when one of its halves' does.
+    // The lse sum is brought to the true maximum once at the end. Skipping most rescales removes 16·D/32 VALU
+    // multiplies per tile, which matters because FP32 MFMA and VALU share the SIMD on gfx950: every VALU cycle
+    // adds to the MFMA time.
     constexpr float kLazy = 8.0f;
-    float m_run = -INFINITY;
-    float mc = -INFINITY; // offset of the state; -inf until the row has a visible key
-    float mcx = 0.0f;     // finite stand-in used in the exponent (masked scores are -inf there, giving 0)
+    const float lazy_raw = kLazy / c2; // kLazy in raw score units
+    float m_half = -INFINITY;
+    float m_lazy = -INFINITY; // re-base when a maximum exceeds this (-inf: any visible key)
+    float mc = -INFINITY;     // offset of the state; -inf until the row has a visible key
+    float mcx = 0.0f;         // finite stand-in used in the exponent (masked scores are -inf there, giving 0)
     float l_run = 0.0f;
     f32x16 o[DT];
 #pragma unroll
@@ -160,21 +166,19 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
             }
         }
 
-        float mx = sc[0];
+        float mx = m_half; // starting from the running maximum folds its update into the three-input maxima
 #pragma unroll
-        for (int j = 1; j < 16; ++j) mx = fmaxf(mx, sc[j]);
-        mx = halves_max(mx);
-        m_run = fmaxf(m_run, mx);
+        for (int j = 0; j < 16; ++j) mx = fmaxf(mx, sc[j]);
+        m_half = mx;
 
         // exp, row sum and PV; instantiated on both sides of the re-base branch so that each side ends in the
         // MFMA chain that writes o (a join after a conditional o *= alpha would cost a copy of o on every tile).
         auto finish = [&]() __attribute__((always_inline)) {
-            float psum = 0.0f;
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                sc[j] = exp2_fast(fmaf(sc[j], c2, -mcx));
-                psum += sc[j];
-            }
+            for (int j = 0; j < 16; ++j) sc[j] = exp2_fast(fmaf(sc[j], c2, -mcx));
+            float psum = sc[0]; // not 0 + sc[0]: the compiler keeps that add (0 + -0 is +0)
+#pragma unroll
+            for (int j = 1; j < 16; ++j) psum += sc[j];
             l_run += psum;
             if constexpr (!STATS) {
 #pragma unroll
@@ -184,10 +188,16 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
                 }
             }
         };
-        if (__ballot(m_run * c2 > mc + kLazy) != 0) {
-            // Re-base every lane on its current maximum. A row without a visible key yet keeps offset -inf (its
+        // The common case (no re-base) is the fall-through path, so the exponentials follow the maxima without a
+        // branch (a jump there also made the compiler wait out the full MFMA result latency again).
+        if (__builtin_expect(__ballot(m_half > m_lazy) == 0, 1)) {
+            finish();
+        } else {
+            // Re-base every lane on its row's current maximum. A row without a visible key yet keeps offset -inf (its
             // l and o are 0); the first finite offset multiplies them by exp2(-inf) = 0.
-            const float mc_new = m_run == -INFINITY ? -INFINITY : m_run * c2;
+            const float m_row = halves_max(m_half);
+            const float mc_new = m_row == -INFINITY ? -INFINITY : m_row * c2;
+            m_lazy = m_row + lazy_raw;
             const float alpha = mc_new == -INFINITY ? 1.0f : exp2_fast(mc - mc_new);
             l_run *= alpha;
             if constexpr (!STATS) {
@@ -196,8 +206,6 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
             }
             mc = mc_new;
             mcx = mc_new == -INFINITY ? 0.0f : mc_new;
-            finish();
-        } else {
             finish();
         }
     };
@@ -215,6 +223,7 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
         step(tb, key0 + split * kTile, ta, key0 + 2 * split * kTile);
     }
     const float mc_run = mc; // offset the wave's (l_run, o) are expressed against
+    const float m_run = halves_max(m_half); // raw maximum of the row over the wave's tiles
 
     // Merge the states of the `split` waves of the item. Every state satisfies l_w = Σ exp2(s·c2 - mc_w); they are
     // combined against the largest offset, and lse's sum is then expressed against the true maximum. The sum runs in

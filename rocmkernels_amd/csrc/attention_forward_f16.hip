@@ -96,8 +96,12 @@ __global__ __launch_bounds__(kThreads) void attention_forward_f16_kernel(const T
 #pragma unroll
     for (int i = 0; i < KC; ++i) qr[i] = load8h<VEC>(qbuf, static_cast<uint32_t>(query) * (2u * q.st) + 2u * (16 * i + 8 * h));
 
+    // Lazy re-basing as in the FP32 forward: m_half is the maximum over this half-wave's keys, the row maximum is
+    // formed only on a re-base and at the end, and m_lazy is the raw score at which p would reach 2^kLazy.
     constexpr float kLazy = 8.0f; // p = exp2(s·c2 - mc) <= 2^8: also within fp16 range
-    float m_run = -INFINITY;
+    const float lazy_raw = kLazy / c2;
+    float m_half = -INFINITY;
+    float m_lazy = -INFINITY;
     float mc = -INFINITY;
     float mcx = 0.0f;
     float l_run = 0.0f;
@@ -162,19 +166,17 @@ __global__ __launch_bounds__(kThreads) void attention_forward_f16_kernel(const T
             }
         }
 
-        float mx = sc[0];
+        float mx = m_half;
 #pragma unroll
-        for (int j = 1; j < 16; ++j) mx = fmaxf(mx, sc[j]);
-        mx = halves_max(mx);
-        m_run = fmaxf(m_run, mx);
+        for (int j = 0; j < 16; ++j) mx = fmaxf(mx, sc[j]);
+        m_half = mx;
 
         auto finish = [&]() __attribute__((always_inline)) {
-            float psum = 0.0f;
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                sc[j] = exp2_fast(fmaf(sc[j], c2, -mcx));
-                psum += sc[j];
-            }
+            for (int j = 0; j < 16; ++j) sc[j] = exp2_fast(fmaf(sc[j], c2, -mcx));
+            float psum = sc[0];
+#pragma unroll
+            for (int j = 1; j < 16; ++j) psum += sc[j];
             l_run += psum;
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
@@ -189,16 +191,18 @@ __global__ __launch_bounds__(kThreads) void attention_forward_f16_kernel(const T
                 for (int t2 = 0; t2 < DT; ++t2) o[t2] = mfma16(t.v[t2][u], p, o[t2]);
             }
         };
-        if (__ballot(m_run * c2 > mc + kLazy) != 0) {
-            const float mc_new = m_run == -INFINITY ? -INFINITY : m_run * c2;
+        if (__builtin_expect(__ballot(m_half > m_lazy) == 0, 1)) {
+            finish();
+        } else {
+            const float m_row = halves_max(m_half);
+            const float mc_new = m_row == -INFINITY ? -INFINITY : m_row * c2;
+            m_lazy = m_row + lazy_raw;
             const float alpha = mc_new == -INFINITY ? 1.0f : exp2_fast(mc - mc_new);
             l_run *= alpha;
 #pragma unroll
             for (int t2 = 0; t2 < DT; ++t2) o[t2] *= alpha;
             mc = mc_new;
             mcx = mc_new == -INFINITY ? 0.0f : mc_new;
-            finish();
-        } else {
             finish();
         }
     };
@@ -212,6 +216,7 @@ __global__ __launch_bounds__(kThreads) void attention_forward_f16_kernel(const T
         step(tb, key0 + SPLIT * kTile, ta, key0 + 2 * SPLIT * kTile);
     }
     const float mc_run = mc;
+    const float m_run = halves_max(m_half);
 
     float m_all = m_run;
     float base = 0.0f, l_all = l_run;
