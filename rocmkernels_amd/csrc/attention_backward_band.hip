@@ -16,10 +16,10 @@
 //   so P = exp2(S chain) and dS = P·(dP chain)), dVᵀ += dOᵀ·P and dKᵀ += Qᵀ·dS,
 // and its own share of dQ for the query tile, dQᵀ = Kᵀ·dSᵀ over its 32 keys: dS goes through the wave's transpose buffer
 // in LDS (queries onto lanes), K's column layout is held in registers (pre-scaled by 1/√D, zero for masked keys). The
-// share is summed in the query tile's slot of a second ring of five LDS tiles. Within a step the four waves work on four
-// different query tiles, and query tile T meets wave 3, 2, 1 and 0 in four consecutive steps, so the sum needs no atomics
-// (LDS float atomics cost several times the step's MFMAs): each wave that sees the tile loads the partial sum as the
-// start of its dQ chain and stores the result. The last contribution comes from wave 0 at step (tile - base); after that
+// share is summed in the query tile's slot of a second ring of five LDS tiles, kept in the accumulator layout. Within a
+// step the four waves work on four different query tiles, and query tile T meets wave 3, 2, 1 and 0 in four consecutive
+// steps, so the sum needs no atomics (LDS float atomics cost several times the step's MFMAs): each wave that sees the
+// tile loads the partial sum as the start of its dQ chain and stores the result. The last contribution comes from wave 0 at step (tile - base); after that
 // step's barrier the four waves add the slot to dQ with FP32 buffer atomics (one add per dQ element per key block, as in
 // the key-block kernel) and zero it, so the ring is zero wherever a walk starts a tile (it is cleared once at the start).
 // Blocks are never split: dK and dV are stored once.
@@ -37,6 +37,11 @@ namespace {
 
 constexpr int kRing = 5;               // query tiles held at once: the four a step reads and the one loaded for the next
 constexpr int kTrStride = kTile + 4;   // transpose buffer row stride: conflict-free row writes and 128-bit row reads
+// dQ partial sums are kept in the accumulator layout every wave shares, lane-major: lane l's 16·D/32 registers at
+// l·kDqStride, so a wave moves its partial sum with 128-bit accesses (four registers each) instead of one float per
+// register; the 4 extra floats per lane keep 16 consecutive lanes of a 128-bit access on distinct banks.
+template<int D>
+constexpr int kDqStride = 16 * (D / 32) + 4;
 
 template<int D>
 struct BandShared {
@@ -44,7 +49,7 @@ struct BandShared {
     float u[kRing][kSlotFloats<D>];            // dO tiles
     float seed_s[kRing][kTile];                // per query: -(m·log2e + log2 l), or -inf where P = 0
     float seed_d[kRing][kTile];                // per query: -δ
-    float dq[kRing][kSlotFloats<D>];           // dQ partial sums of the query tiles in flight, [query][feature]
+    float dq[kRing][kWave * kDqStride<D>];     // dQ partial sums of the query tiles in flight, [lane][register]
     float tr[kBlockTiles][kTile * kTrStride];  // per wave: dS transposed, [query][key]
 };
 
@@ -75,7 +80,7 @@ __global__ __launch_bounds__(kWave * kBlockTiles) void attention_band_backward_k
     const uint32_t kstep = 4u * k.st, vstep = 4u * v.st, qstep = 4u * q.st, ustep = 4u * du.st;
 
     // The dQ ring starts at zero; every flush zeroes the slot it empties (the first block's barrier orders these stores).
-    for (int e = 4 * static_cast<int>(threadIdx.x); e < kRing * kSlotFloats<D>; e += 4 * kWave * kBlockTiles)
+    for (int e = 4 * static_cast<int>(threadIdx.x); e < kRing * kWave * kDqStride<D>; e += 4 * kWave * kBlockTiles)
         *reinterpret_cast<f32x4 *>(&sh.dq[0][0] + e) = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     const int group = static_cast<int>(blockIdx.x) % groups;
     const int member = static_cast<int>(blockIdx.x) / groups;
@@ -158,24 +163,25 @@ __global__ __launch_bounds__(kWave * kBlockTiles) void attention_band_backward_k
             sh.seed_s[slot][row] = ok ? seed : -INFINITY; // P = exp2(S·scale·log2e + this)
             sh.seed_d[slot][row] = -r.d;
         };
-        // Adds query tile X's finished dQ slot into dQ (each wave a quarter: 8 rows, whole lines per instruction) and
-        // zeroes it. Tiles outside the sequence, or that no wave of the block touched, hold zeros and are skipped.
+        // Adds query tile X's finished dQ slot into dQ and zeroes it. Wave w takes registers RQ·w .. RQ·w + RQ - 1 of
+        // every lane: register (t, j) of lane (col, h) is query tile_row(j, h), feature 32t + col, so each atomic
+        // instruction covers two whole 128-byte rows. Tiles outside the sequence, or that no wave of the block touched,
+        // hold zeros and are skipped.
         auto flush = [&](const int tile) __attribute__((always_inline)) {
             if (tile < 0 || tile >= qtiles || tile < union_lo || tile >= union_hi) return;
-            float *slot = sh.dq[(tile + kRing) % kRing];
-            float x[D / 8];
+            constexpr int RQ = 4 * DT; // registers per wave: a quarter of the lane's 16·DT
+            f32x4 *src = reinterpret_cast<f32x4 *>(&sh.dq[(tile + kRing) % kRing][lane * kDqStride<D> + RQ * w]);
+            f32x4 x[RQ / 4];
 #pragma unroll
-            for (int r = 0; r < D / 8; ++r) {
-                const int e = r * kWave + lane;
-                x[r] = slot[(8 * w + e / D) * S + e % D];
-                slot[(8 * w + e / D) * S + e % D] = 0.0f;
+            for (int c = 0; c < RQ / 4; ++c) {
+                x[c] = src[c];
+                src[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
             }
 #pragma unroll
-            for (int r = 0; r < D / 8; ++r) {
-                const int e = r * kWave + lane;
-                const int row = 8 * w + e / D, feature = e % D;
-                const uint32_t voff = (static_cast<uint32_t>(tile * kTile + row) * D + static_cast<uint32_t>(feature)) * 4u;
-                __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(x[r], qgbuf, static_cast<int>(voff), 0, 0);
+            for (int r = 0; r < RQ; ++r) {
+                const int reg = RQ * w + r, t = reg >> 4, j = reg & 15;
+                const uint32_t voff = (static_cast<uint32_t>(tile * kTile + tile_row(j, h)) * D + static_cast<uint32_t>(32 * t + col)) * 4u;
+                __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(x[r >> 2][r & 3], qgbuf, static_cast<int>(voff), 0, 0);
             }
         };
 
@@ -297,8 +303,8 @@ __global__ __launch_bounds__(kWave * kBlockTiles) void attention_band_backward_k
                     }
                     wave_lds_sync();
                     // dQ share of this key tile, dS·K over its 32 keys (A = dS rows, B = K's column layout), chained onto the
-                    // query tile's partial sum: register j of slice t is query q0 + tile_row(j, h), feature 32t + col, so each
-                    // LDS access covers 32 consecutive features of two rows.
+                    // query tile's partial sum: register j of slice t is query q0 + tile_row(j, h), feature 32t + col, and the
+                    // partial sum is read and written in that register layout (four registers per 128-bit access).
                     float bq[16];
                     f32x16 acc_q[DT];
     #pragma unroll
@@ -309,10 +315,15 @@ __global__ __launch_bounds__(kWave * kBlockTiles) void attention_band_backward_k
                         bq[4 * u + 2] = x[2];
                         bq[4 * u + 3] = x[3];
                     }
+                    f32x4 *const mine = reinterpret_cast<f32x4 *>(dslot + lane * kDqStride<D>);
     #pragma unroll
                     for (int t = 0; t < DT; ++t) {
     #pragma unroll
-                        for (int j = 0; j < 16; ++j) acc_q[t][j] = dslot[tile_row(j, h) * S + 32 * t + col];
+                        for (int u = 0; u < 4; ++u) {
+                            const f32x4 x = mine[4 * t + u];
+    #pragma unroll
+                            for (int e = 0; e < 4; ++e) acc_q[t][4 * u + e] = x[e];
+                        }
                     }
                     __builtin_amdgcn_sched_barrier(0);
     #pragma unroll
@@ -323,7 +334,8 @@ __global__ __launch_bounds__(kWave * kBlockTiles) void attention_band_backward_k
     #pragma unroll
                     for (int t = 0; t < DT; ++t) {
     #pragma unroll
-                        for (int j = 0; j < 16; ++j) dslot[tile_row(j, h) * S + 32 * t + col] = acc_q[t][j];
+                        for (int u = 0; u < 4; ++u)
+                            mine[4 * t + u] = f32x4{acc_q[t][4 * u], acc_q[t][4 * u + 1], acc_q[t][4 * u + 2], acc_q[t][4 * u + 3]};
                     }
                 }
                 if (has_next) store_quarter(next, base + i + kBlockTiles);
