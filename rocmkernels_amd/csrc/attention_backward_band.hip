@@ -19,9 +19,10 @@
 // share is summed in the query tile's slot of a second ring of five LDS tiles, kept in the accumulator layout. Within a
 // step the four waves work on four different query tiles, and query tile T meets wave 3, 2, 1 and 0 in four consecutive
 // steps, so the sum needs no atomics (LDS float atomics cost several times the step's MFMAs): each wave that sees the
-// tile loads the partial sum as the start of its dQ chain and stores the result. The last contribution comes from wave 0 at step (tile - base); after that
-// step's barrier the four waves add the slot to dQ with FP32 buffer atomics (one add per dQ element per key block, as in
-// the key-block kernel) and zero it, so the ring is zero wherever a walk starts a tile (it is cleared once at the start).
+// tile loads the partial sum as the start of its dQ chain and stores the result. The last contribution comes from wave 0
+// at step (tile - base); after that step's barrier the four waves add the slot to dQ with FP32 buffer atomics (one add
+// per dQ element per key block, as in the key-block kernel) and zero it, so the ring is zero wherever a walk starts a
+// tile (it is cleared once at the start).
 // Blocks are never split: dK and dV are stored once.
 //
 // Work mapping: one persistent workgroup per CU walks the blocks g, g + G, ...; with the sequences and the grid divisible
@@ -59,6 +60,52 @@ struct BandQuarter {
     f32x4 q[D / 32], u[D / 32];
     float m, l, d;
 };
+
+// At D = 64 the Q and dO rows of the ring interleave the two 32-feature halves: feature f sits at position
+// 2 (f mod 32) + f / 32. A lane's column-layout operands for both output slices (features col and 32 + col of a row)
+// are then one 64-bit read instead of two 32-bit reads. The S and dP products reduce over the positions in order, so
+// the K and V rows they pair with are loaded in the same order (load_row_positions).
+template<int D>
+constexpr bool kInterleaved = D == 64;
+
+// Row of HALF = D/2 positions for half-wave h of a row in natural feature order at byte offset `row`: positions
+// 32h .. 32h + 31 of the interleaved order, i.e. features 16h + m and 32 + 16h + m at r[2m] and r[2m + 1].
+template<int D>
+__device__ __forceinline__ void load_row_positions(float (&r)[D / 2], const Buffer b, const uint32_t row, const int h) {
+    if constexpr (kInterleaved<D>) {
+        float lo[16], hi[16];
+        buffer_load_span<true>(lo, b, row + 64u * static_cast<uint32_t>(h));
+        buffer_load_span<true>(hi, b, row + 128u + 64u * static_cast<uint32_t>(h));
+#pragma unroll
+        for (int m = 0; m < 16; ++m) {
+            r[2 * m] = lo[m];
+            r[2 * m + 1] = hi[m];
+        }
+    } else {
+        buffer_load_span<true>(r, b, row + 4u * static_cast<uint32_t>(h) * (D / 2));
+    }
+}
+
+// Column layout of an interleaved slot: element [tile_row(j, h)][32t + col] to c[t][j - J0], both slices with one
+// 64-bit read per row (the A operands of MFMAs j of a product that reduces over the slot's rows).
+template<int D, int J0, int J>
+__device__ __forceinline__ void read_column_pairs(const float *slot, float (&c)[D / 32][J]) {
+    static_assert(D == 64, "two 32-feature slices");
+    const int lane = threadIdx.x & (kWave - 1);
+    const float *base = slot + 4 * (lane >> 5) * kSlotStride<D> + 2 * (lane & 31);
+#pragma unroll
+    for (int j = J0; j < J0 + J; ++j) {
+        const f32x2 x = *reinterpret_cast<const f32x2 *>(base + (8 * (j >> 2) + (j & 3)) * kSlotStride<D>);
+        c[0][j - J0] = x[0];
+        c[1][j - J0] = x[1];
+    }
+}
+
+template<int D, int J0, int J>
+__device__ __forceinline__ void read_columns(const float *slot, float (&c)[D / 32][J]) {
+    if constexpr (kInterleaved<D>) read_column_pairs<D, J0, J>(slot, c);
+    else read_column_layout<D, J0, J>(slot, c);
+}
 
 template<int D>
 __global__ __launch_bounds__(kWave * kBlockTiles) void attention_band_backward_kernel(const Tensor q, const Tensor k,
@@ -116,9 +163,9 @@ __global__ __launch_bounds__(kWave * kBlockTiles) void attention_band_backward_k
 
         // K and V rows of this wave's key tile (row layout: B operands of S and dP), K pre-scaled by scale·log2e; K's
         // column layout (A operand of dQᵀ), pre-scaled by 1/√D and zero for masked keys, whatever K holds there.
-        float kr[HALF], vr[HALF];
-        buffer_load_span<true>(kr, kbuf, in_range ? static_cast<uint32_t>(key) * kstep + 4u * h * HALF : kNoRow);
-        buffer_load_span<true>(vr, vbuf, in_range ? static_cast<uint32_t>(key) * vstep + 4u * h * HALF : kNoRow);
+        float kr[HALF], vr[HALF]; // in the ring's position order (kInterleaved)
+        load_row_positions<D>(kr, kbuf, in_range ? static_cast<uint32_t>(key) * kstep : kNoRow, h);
+        load_row_positions<D>(vr, vbuf, in_range ? static_cast<uint32_t>(key) * vstep : kNoRow, h);
         float kc[DT][16];
         {
             const uint32_t klane = static_cast<uint32_t>(key0 + 4 * h) * kstep + 4u * col;
@@ -149,11 +196,22 @@ __global__ __launch_bounds__(kWave * kBlockTiles) void attention_band_backward_k
         auto store_quarter = [&](const BandQuarter<D> &r, const int tile) __attribute__((always_inline)) {
             const int slot = (tile + kRing) % kRing;
             const int row = 8 * w + (lane & 7);
+            if constexpr (kInterleaved<D>) {
+                // The lane holds features 4c .. 4c + 3 and 32 + 4c .. 32 + 4c + 3 (c = lane / 8): positions 8c .. 8c + 7.
+                const int at = row * S + 8 * (lane >> 3);
+                auto put = [&](float *dst, const f32x4 (&x)[D / 32]) __attribute__((always_inline)) {
+                    *reinterpret_cast<f32x4 *>(dst + at) = f32x4{x[0][0], x[1][0], x[0][1], x[1][1]};
+                    *reinterpret_cast<f32x4 *>(dst + at + 4) = f32x4{x[0][2], x[1][2], x[0][3], x[1][3]};
+                };
+                put(sh.q[slot], r.q);
+                put(sh.u[slot], r.u);
+            } else {
 #pragma unroll
-            for (int i = 0; i < D / 32; ++i) {
-                const int at = row * S + 4 * (8 * i + (lane >> 3));
-                *reinterpret_cast<f32x4 *>(&sh.q[slot][at]) = r.q[i];
-                *reinterpret_cast<f32x4 *>(&sh.u[slot][at]) = r.u[i];
+                for (int i = 0; i < D / 32; ++i) {
+                    const int at = row * S + 4 * (8 * i + (lane >> 3));
+                    *reinterpret_cast<f32x4 *>(&sh.q[slot][at]) = r.q[i];
+                    *reinterpret_cast<f32x4 *>(&sh.u[slot][at]) = r.u[i];
+                }
             }
             const int query = tile * kTile + row;
             const bool ok = query >= 0 && query < s.queries && r.m != -INFINITY;
@@ -285,17 +343,17 @@ __global__ __launch_bounds__(kWave * kBlockTiles) void attention_band_backward_k
                     };
                     {
                         float ca[DT][8], cb[DT][8];
-                        read_column_layout<D, 0, 8>(sh.u[slot], ca);
+                        read_columns<D, 0, 8>(sh.u[slot], ca);
                         __builtin_amdgcn_sched_barrier(0);
-                        read_column_layout<D, 8, 8>(sh.u[slot], cb);
+                        read_columns<D, 8, 8>(sh.u[slot], cb);
                         __builtin_amdgcn_sched_barrier(0);
                         products(ca, sc, 0, acc_v);
                         __builtin_amdgcn_sched_barrier(0);
-                        read_column_layout<D, 0, 8>(sh.q[slot], ca);
+                        read_columns<D, 0, 8>(sh.q[slot], ca);
                         __builtin_amdgcn_sched_barrier(0);
                         products(cb, sc, 8, acc_v);
                         __builtin_amdgcn_sched_barrier(0);
-                        read_column_layout<D, 8, 8>(sh.q[slot], cb);
+                        read_columns<D, 8, 8>(sh.q[slot], cb);
                         __builtin_amdgcn_sched_barrier(0);
                         products(ca, dp, 0, acc_k);
                         __builtin_amdgcn_sched_barrier(0);
