@@ -133,66 +133,95 @@ __global__ __launch_bounds__(kWave * kBlockTiles) void attention_band_backward_k
     const int member = static_cast<int>(blockIdx.x) / groups;
     const int members = static_cast<int>(gridDim.x) / groups;
     const int group_blocks = seqs / groups * nblocks;
-    for (int index = member; index < group_blocks; index += members) {
+    // A block's coordinates and the buffer resources of its sequence.
+    struct Block {
+        int seq, kb;
+        Buffer kbuf, vbuf, qbuf, ubuf, lbuf, dbuf, mbuf;
+        BandWalk walk;
+    };
+    auto block_at = [&](const int index) __attribute__((always_inline)) {
+        Block c;
         const int local_seq = index / nblocks;
-        const int kb = index - local_seq * nblocks;
-        const int seq = group + groups * local_seq;
-        const int b = seq / s.heads;
-        const int head = seq - b * s.heads;
-        const Buffer kbuf = make_buffer(sequence(k, b, head), sequence_bytes(s.keys, k.st, D));
-        const Buffer vbuf = make_buffer(sequence(v, b, head), sequence_bytes(s.keys, v.st, D));
-        const Buffer qbuf = make_buffer(sequence(q, b, head), sequence_bytes(s.queries, q.st, D));
-        const Buffer ubuf = make_buffer(sequence(du, b, head), sequence_bytes(s.queries, du.st, D));
-        const Buffer lbuf = make_buffer(lse + static_cast<int64_t>(seq) * s.queries * 2, static_cast<uint32_t>(s.queries) * 8u);
-        const Buffer dbuf = make_buffer(delta + static_cast<int64_t>(seq) * s.queries, static_cast<uint32_t>(s.queries) * 4u);
-        const Buffer mbuf = make_buffer(mask + static_cast<int64_t>(b) * s.keys, static_cast<uint32_t>(s.keys));
-        const Buffer qgbuf = make_buffer(dq + static_cast<int64_t>(seq) * s.queries * D, static_cast<uint32_t>(s.queries) * (4u * D));
+        c.kb = index - local_seq * nblocks;
+        c.seq = group + groups * local_seq;
+        const int b = c.seq / s.heads;
+        const int head = c.seq - b * s.heads;
+        c.kbuf = make_buffer(sequence(k, b, head), sequence_bytes(s.keys, k.st, D));
+        c.vbuf = make_buffer(sequence(v, b, head), sequence_bytes(s.keys, v.st, D));
+        c.qbuf = make_buffer(sequence(q, b, head), sequence_bytes(s.queries, q.st, D));
+        c.ubuf = make_buffer(sequence(du, b, head), sequence_bytes(s.queries, du.st, D));
+        c.lbuf = make_buffer(lse + static_cast<int64_t>(c.seq) * s.queries * 2, static_cast<uint32_t>(s.queries) * 8u);
+        c.dbuf = make_buffer(delta + static_cast<int64_t>(c.seq) * s.queries, static_cast<uint32_t>(s.queries) * 4u);
+        c.mbuf = make_buffer(mask + static_cast<int64_t>(b) * s.keys, static_cast<uint32_t>(s.keys));
+        // The skewed schedule (step i, wave w: query tile base + i + w) and the union of the bands.
+        c.walk = band_walk(s.queries, s.keys, s.radius, s.causal, c.kb);
+        return c;
+    };
+    // Query-tile quarters: rows 8w .. 8w + 7 of tile T, lane (row lane % 8, 16-byte chunk 8i + lane / 8), whole lines.
+    // Rows outside the sequence (T < 0 or past the end) read 0 and get P = 0.
+    auto load_quarter = [&](const Block &c, BandQuarter<D> &r, const int tile) __attribute__((always_inline)) {
+        const int query = tile * kTile + 8 * w + (lane & 7);
+        const bool ok = query >= 0 && query < s.queries; // kNoRow keeps the offset out of range for any stride
+        const uint32_t row = static_cast<uint32_t>(query);
+#pragma unroll
+        for (int i = 0; i < D / 32; ++i) {
+            const uint32_t chunk = static_cast<uint32_t>(8 * i + (lane >> 3));
+            r.q[i] = buffer_load4(c.qbuf, (ok ? row * qstep : kNoRow) + 16u * chunk, 0);
+            r.u[i] = buffer_load4(c.ubuf, (ok ? row * ustep : kNoRow) + 16u * chunk, 0);
+        }
+        r.m = buffer_load(c.lbuf, ok ? row * 8u : kNoRow, 0);
+        r.l = buffer_load(c.lbuf, ok ? row * 8u + 4u : kNoRow, 0);
+        r.d = buffer_load(c.dbuf, ok ? row * 4u : kNoRow, 0);
+    };
+    // The loads a block starts from: the key-mask byte (keys past the end read 0 through kNoRow rather than a branch),
+    // this wave's K and V rows (row layout: B operands of S and dP), K's column layout (A operand of dQᵀ) and the first
+    // four query tiles' quarters. The next block's are issued as soon as a walk ends, before the walk's last dQ adds
+    // and the dK/dV stores: their round trip overlaps the end of the block, and the in-order vector-memory counter
+    // does not make the next block wait for those adds (all 256 workgroups end their blocks together, so the adds
+    // arrive at the L2 as one burst).
+    struct BlockLoads {
+        int mask_byte;
+        float kr[HALF], vr[HALF]; // in the ring's position order (kInterleaved)
+        float kc[DT][16];
+        BandQuarter<D> opening[kBlockTiles];
+    };
+    auto issue = [&](const Block &c, BlockLoads &ld) __attribute__((always_inline)) {
+        const int key0 = (c.kb * kBlockTiles + w) * kTile;
+        const int key = key0 + col;
+        const bool in_range = key < s.keys;
+        ld.mask_byte = buffer_load_byte(c.mbuf, in_range ? static_cast<uint32_t>(key) : kNoRow);
+        load_row_positions<D>(ld.kr, c.kbuf, in_range ? static_cast<uint32_t>(key) * kstep : kNoRow, h);
+        load_row_positions<D>(ld.vr, c.vbuf, in_range ? static_cast<uint32_t>(key) * vstep : kNoRow, h);
+        const uint32_t klane = static_cast<uint32_t>(key0 + 4 * h) * kstep + 4u * col;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+#pragma unroll
+            for (int t = 0; t < DT; ++t)
+                ld.kc[t][j] = buffer_load(c.kbuf, klane + 128u * t, static_cast<uint32_t>(8 * (j >> 2) + (j & 3)) * kstep);
+        }
+        // A block that no query sees reads nothing (its tiles would be outside every band).
+        const int base = c.walk.nsteps > 0 ? c.walk.base : -0x10000;
+#pragma unroll
+        for (int x = 0; x < kBlockTiles; ++x) load_quarter(c, ld.opening[x], base + x);
+    };
 
-        // The skewed schedule (step i, wave w: query tile base + i + w), this wave's band and the union of the bands.
-        const BandWalk walk = band_walk(s.queries, s.keys, s.radius, s.causal, kb);
-        const int base = walk.base, nsteps = walk.nsteps, union_lo = walk.lo, union_hi = walk.hi;
-        int my_first, my_end;
+    BlockLoads ld;
+    if (member < group_blocks) issue(block_at(member), ld);
+    for (int index = member; index < group_blocks; index += members) {
+        const Block cur = block_at(index);
+        const int seq = cur.seq, kb = cur.kb;
+        const Buffer qgbuf = make_buffer(dq + static_cast<int64_t>(seq) * s.queries * D, static_cast<uint32_t>(s.queries) * (4u * D));
+        const int base = cur.walk.base, nsteps = cur.walk.nsteps, union_lo = cur.walk.lo, union_hi = cur.walk.hi;
+        int my_first, my_end; // this wave's band
         key_tile_band(s.queries, s.keys, s.radius, s.causal, kb * kBlockTiles + w, my_first, my_end);
 
         const int key0 = (kb * kBlockTiles + w) * kTile;
         const int key = key0 + col;
-        const bool in_range = key < s.keys;
-        // Every load of the block is issued before the first wait (the mask byte too: keys past the end read 0 through
-        // kNoRow rather than a branch), so the block start costs one memory round trip.
-        const int mask_byte = buffer_load_byte(mbuf, in_range ? static_cast<uint32_t>(key) : kNoRow);
-
-        // K and V rows of this wave's key tile (row layout: B operands of S and dP), K pre-scaled by scale·log2e; K's
-        // column layout (A operand of dQᵀ), pre-scaled by 1/√D and zero for masked keys, whatever K holds there.
-        float kr[HALF], vr[HALF]; // in the ring's position order (kInterleaved)
-        load_row_positions<D>(kr, kbuf, in_range ? static_cast<uint32_t>(key) * kstep : kNoRow, h);
-        load_row_positions<D>(vr, vbuf, in_range ? static_cast<uint32_t>(key) * vstep : kNoRow, h);
-        float kc[DT][16];
-        {
-            const uint32_t klane = static_cast<uint32_t>(key0 + 4 * h) * kstep + 4u * col;
-#pragma unroll
-            for (int j = 0; j < 16; ++j) {
-#pragma unroll
-                for (int t = 0; t < DT; ++t)
-                    kc[t][j] = buffer_load(kbuf, klane + 128u * t, static_cast<uint32_t>(8 * (j >> 2) + (j & 3)) * kstep);
-            }
-        }
-
-        // Query-tile quarters: rows 8w .. 8w + 7 of tile T, lane (row lane % 8, 16-byte chunk 8i + lane / 8), whole lines.
-        // Rows outside the sequence (T < 0 or past the end) read 0 and get P = 0.
-        auto load_quarter = [&](BandQuarter<D> &r, const int tile) __attribute__((always_inline)) {
-            const int query = tile * kTile + 8 * w + (lane & 7);
-            const bool ok = query >= 0 && query < s.queries; // kNoRow keeps the offset out of range for any stride
-            const uint32_t row = static_cast<uint32_t>(query);
-#pragma unroll
-            for (int i = 0; i < D / 32; ++i) {
-                const uint32_t chunk = static_cast<uint32_t>(8 * i + (lane >> 3));
-                r.q[i] = buffer_load4(qbuf, (ok ? row * qstep : kNoRow) + 16u * chunk, 0);
-                r.u[i] = buffer_load4(ubuf, (ok ? row * ustep : kNoRow) + 16u * chunk, 0);
-            }
-            r.m = buffer_load(lbuf, ok ? row * 8u : kNoRow, 0);
-            r.l = buffer_load(lbuf, ok ? row * 8u + 4u : kNoRow, 0);
-            r.d = buffer_load(dbuf, ok ? row * 4u : kNoRow, 0);
-        };
+        // K pre-scaled by scale·log2e below; K's column layout pre-scaled by 1/√D and zero for masked keys, whatever K
+        // holds there.
+        float (&kr)[HALF] = ld.kr;
+        float (&vr)[HALF] = ld.vr;
+        float (&kc)[DT][16] = ld.kc;
         auto store_quarter = [&](const BandQuarter<D> &r, const int tile) __attribute__((always_inline)) {
             const int slot = (tile + kRing) % kRing;
             const int row = 8 * w + (lane & 7);
@@ -249,12 +278,7 @@ __global__ __launch_bounds__(kWave * kBlockTiles) void attention_band_backward_k
             acc_k[t] = f32x16{};
             acc_v[t] = f32x16{};
         }
-        BandQuarter<D> opening[kBlockTiles]; // the first four query tiles of the walk
-        if (nsteps > 0) {
-    #pragma unroll
-            for (int x = 0; x < kBlockTiles; ++x) load_quarter(opening[x], base + x);
-        }
-        const bool visible = mask_byte != 0;
+        const bool visible = ld.mask_byte != 0;
         const uint32_t bits = static_cast<uint32_t>(__ballot(visible));
         if (bits == 0) my_end = my_first; // no visible key: the wave only keeps the schedule
         const int qlo = window_query_lo(s, key);
@@ -267,7 +291,7 @@ __global__ __launch_bounds__(kWave * kBlockTiles) void attention_band_backward_k
         }
         if (nsteps > 0) { // a block that no query sees stores zero dK/dV below
     #pragma unroll
-            for (int x = 0; x < kBlockTiles; ++x) store_quarter(opening[x], base + x);
+            for (int x = 0; x < kBlockTiles; ++x) store_quarter(ld.opening[x], base + x);
     #pragma unroll
             for (int c = 0; c < HALF; ++c) kr[c] *= c2;
             __syncthreads();
@@ -279,7 +303,7 @@ __global__ __launch_bounds__(kWave * kBlockTiles) void attention_band_backward_k
                 const bool has_next = i + 1 < nsteps;
                 float *const dslot = sh.dq[slot];
                 BandQuarter<D> next;
-                if (has_next) load_quarter(next, base + i + kBlockTiles);
+                if (has_next) load_quarter(cur, next, base + i + kBlockTiles);
                 if (tile >= my_first && tile < my_end) {
                     const int q0 = tile * kTile;
                     // Each product's LDS reads are issued together, ahead of its MFMAs (sched_barrier keeps them there):
@@ -400,6 +424,10 @@ __global__ __launch_bounds__(kWave * kBlockTiles) void attention_band_backward_k
                 __syncthreads(); // this step's dQ shares and the next step's tile are in LDS
                 flush(base + i); // wave 0 has just given query tile base + i its last share
             }
+        }
+        // This block's K/V rows and column layout are dead: the next block's loads go out now (see BlockLoads).
+        if (index + members < group_blocks) issue(block_at(index + members), ld);
+        if (nsteps > 0) {
             // Query tiles still in flight after the walk: only waves 1..3 reached them.
     #pragma unroll
             for (int x = 0; x < kBlockTiles - 1; ++x) flush(base + nsteps + x);
