@@ -174,31 +174,21 @@ __global__ __launch_bounds__(kWave * kBlockTiles) void attention_band_backward_k
         r.d = buffer_load(c.dbuf, ok ? row * 4u : kNoRow, 0);
     };
     // The loads a block starts from: the key-mask byte (keys past the end read 0 through kNoRow rather than a branch),
-    // this wave's K and V rows (row layout: B operands of S and dP), K's column layout (A operand of dQᵀ) and the first
-    // four query tiles' quarters. The next block's are issued as soon as a walk ends, before the walk's last dQ adds
-    // and the dK/dV stores: their round trip overlaps the end of the block, and the in-order vector-memory counter
-    // does not make the next block wait for those adds (all 256 workgroups end their blocks together, so the adds
-    // arrive at the L2 as one burst).
+    // this wave's K and V rows (row layout: B operands of S and dP) and the first four query tiles' quarters. The next
+    // block's are issued as soon as a walk ends, before the walk's last dQ adds and the dK/dV stores: their round trip
+    // overlaps the end of the block, and the in-order vector-memory counter does not make the next block wait for
+    // those adds (all 256 workgroups end their blocks together, so the adds arrive at the L2 as one burst).
     struct BlockLoads {
         int mask_byte;
         float kr[HALF], vr[HALF]; // in the ring's position order (kInterleaved)
-        float kc[DT][16];
         BandQuarter<D> opening[kBlockTiles];
     };
     auto issue = [&](const Block &c, BlockLoads &ld) __attribute__((always_inline)) {
-        const int key0 = (c.kb * kBlockTiles + w) * kTile;
-        const int key = key0 + col;
+        const int key = (c.kb * kBlockTiles + w) * kTile + col;
         const bool in_range = key < s.keys;
         ld.mask_byte = buffer_load_byte(c.mbuf, in_range ? static_cast<uint32_t>(key) : kNoRow);
         load_row_positions<D>(ld.kr, c.kbuf, in_range ? static_cast<uint32_t>(key) * kstep : kNoRow, h);
         load_row_positions<D>(ld.vr, c.vbuf, in_range ? static_cast<uint32_t>(key) * vstep : kNoRow, h);
-        const uint32_t klane = static_cast<uint32_t>(key0 + 4 * h) * kstep + 4u * col;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-#pragma unroll
-            for (int t = 0; t < DT; ++t)
-                ld.kc[t][j] = buffer_load(c.kbuf, klane + 128u * t, static_cast<uint32_t>(8 * (j >> 2) + (j & 3)) * kstep);
-        }
         // A block that no query sees reads nothing (its tiles would be outside every band).
         const int base = c.walk.nsteps > 0 ? c.walk.base : -0x10000;
 #pragma unroll
@@ -217,11 +207,31 @@ __global__ __launch_bounds__(kWave * kBlockTiles) void attention_band_backward_k
 
         const int key0 = (kb * kBlockTiles + w) * kTile;
         const int key = key0 + col;
-        // K pre-scaled by scale·log2e below; K's column layout pre-scaled by 1/√D and zero for masked keys, whatever K
-        // holds there.
-        float (&kr)[HALF] = ld.kr;
+        float (&kr)[HALF] = ld.kr; // pre-scaled by scale·log2e below
         float (&vr)[HALF] = ld.vr;
-        float (&kc)[DT][16] = ld.kc;
+        // K's column layout (A operand of dQᵀ: kc[t][j] = K[key0 + tile_row(j, h)][32t + col]) from the row layout,
+        // one 32-feature slice at a time through this wave's transpose buffer (free until the walk): 4 128-bit writes
+        // and 16 reads per slice instead of 16 single-float loads per slice from memory. Pre-scaled by 1/√D and zero
+        // for masked keys below, whatever K holds there.
+        float kc[DT][16];
+        {
+            float *const tb = sh.tr[w];
+#pragma unroll
+            for (int t = 0; t < DT; ++t) {
+                wave_lds_sync(); // the previous slice's reads (or the previous block's walk) are done
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    // Lane (key col, h) holds features 32t + 16h + 4u .. +3 (positions 2m + t at D = 64, m otherwise).
+                    f32x4 x;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) x[e] = kInterleaved<D> ? kr[2 * (4 * u + e) + t] : kr[4 * u + e];
+                    *reinterpret_cast<f32x4 *>(&tb[col * kTrStride + 16 * h + 4 * u]) = x;
+                }
+                wave_lds_sync();
+#pragma unroll
+                for (int j = 0; j < 16; ++j) kc[t][j] = tb[tile_row(j, h) * kTrStride + col];
+            }
+        }
         auto store_quarter = [&](const BandQuarter<D> &r, const int tile) __attribute__((always_inline)) {
             const int slot = (tile + kRing) % kRing;
             const int row = 8 * w + (lane & 7);
