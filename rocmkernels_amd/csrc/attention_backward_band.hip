@@ -195,6 +195,29 @@ __global__ __launch_bounds__(kWave * kBlockTiles) void attention_band_backward_k
         for (int x = 0; x < kBlockTiles; ++x) load_quarter(c, ld.opening[x], base + x);
     };
 
+    // Adds this wave's quarter of a finished dQ tile into dQ: wave w holds registers RQ·w .. RQ·w + RQ - 1 of every
+    // lane, and register (t, j) of lane (col, h) is query tile_row(j, h), feature 32t + col, so each atomic instruction
+    // covers two whole 128-byte rows.
+    constexpr int RQ = 4 * DT; // registers per wave: a quarter of the lane's 16·DT
+    auto add_tile = [&](const Buffer gbuf, const int tile, const f32x4 (&x)[RQ / 4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int r = 0; r < RQ; ++r) {
+            const int reg = RQ * w + r, t = reg >> 4, j = reg & 15;
+            const uint32_t voff = (static_cast<uint32_t>(tile * kTile + tile_row(j, h)) * D + static_cast<uint32_t>(32 * t + col)) * 4u;
+            __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(x[r >> 2][r & 3], gbuf, static_cast<int>(voff), 0, 0);
+        }
+    };
+    // The three query tiles still in flight when a walk ends are taken out of the ring at the block's end, but their
+    // adds go out during the next block's first three steps, one tile per step: every workgroup ends its blocks at the
+    // same time, and adding all three at once made each block end one burst of FP32 atomics on the L2.
+    f32x4 tail[kBlockTiles - 1][RQ / 4];
+    int tail_tile[kBlockTiles - 1] = {-1, -1, -1}; // -1: nothing pending
+    Buffer tail_buf = make_buffer(dq, 0);           // dQ of the sequence the pending tiles belong to
+    auto emit = [&](const int x) __attribute__((always_inline)) {
+        if (tail_tile[x] >= 0) add_tile(tail_buf, tail_tile[x], tail[x]);
+        tail_tile[x] = -1;
+    };
+
     BlockLoads ld;
     if (member < group_blocks) issue(block_at(member), ld);
     for (int index = member; index < group_blocks; index += members) {
@@ -260,26 +283,21 @@ __global__ __launch_bounds__(kWave * kBlockTiles) void attention_band_backward_k
             sh.seed_s[slot][row] = ok ? seed : -INFINITY; // P = exp2(S·scale·log2e + this)
             sh.seed_d[slot][row] = -r.d;
         };
-        // Adds query tile X's finished dQ slot into dQ and zeroes it. Wave w takes registers RQ·w .. RQ·w + RQ - 1 of
-        // every lane: register (t, j) of lane (col, h) is query tile_row(j, h), feature 32t + col, so each atomic
-        // instruction covers two whole 128-byte rows. Tiles outside the sequence, or that no wave of the block touched,
-        // hold zeros and are skipped.
-        auto flush = [&](const int tile) __attribute__((always_inline)) {
-            if (tile < 0 || tile >= qtiles || tile < union_lo || tile >= union_hi) return;
-            constexpr int RQ = 4 * DT; // registers per wave: a quarter of the lane's 16·DT
+        // Takes query tile X's finished dQ slot (this wave's quarter) and zeroes it; false for tiles outside the
+        // sequence or that no wave of the block touched (they hold zeros).
+        auto take = [&](const int tile, f32x4 (&x)[RQ / 4]) __attribute__((always_inline)) {
+            if (tile < 0 || tile >= qtiles || tile < union_lo || tile >= union_hi) return false;
             f32x4 *src = reinterpret_cast<f32x4 *>(&sh.dq[(tile + kRing) % kRing][lane * kDqStride<D> + RQ * w]);
-            f32x4 x[RQ / 4];
 #pragma unroll
             for (int c = 0; c < RQ / 4; ++c) {
                 x[c] = src[c];
                 src[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
             }
-#pragma unroll
-            for (int r = 0; r < RQ; ++r) {
-                const int reg = RQ * w + r, t = reg >> 4, j = reg & 15;
-                const uint32_t voff = (static_cast<uint32_t>(tile * kTile + tile_row(j, h)) * D + static_cast<uint32_t>(32 * t + col)) * 4u;
-                __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(x[r >> 2][r & 3], qgbuf, static_cast<int>(voff), 0, 0);
-            }
+            return true;
+        };
+        auto flush = [&](const int tile) __attribute__((always_inline)) {
+            f32x4 x[RQ / 4];
+            if (take(tile, x)) add_tile(qgbuf, tile, x);
         };
 
         f32x16 acc_k[DT], acc_v[DT];
@@ -433,14 +451,27 @@ __global__ __launch_bounds__(kWave * kBlockTiles) void attention_band_backward_k
                 if (has_next) store_quarter(next, base + i + kBlockTiles);
                 __syncthreads(); // this step's dQ shares and the next step's tile are in LDS
                 flush(base + i); // wave 0 has just given query tile base + i its last share
+                // The previous block's last tiles, one per step.
+                if (i == 0) emit(0);
+                else if (i == 1) emit(1);
+                else if (i == 2) emit(2);
             }
         }
+#pragma unroll
+        for (int x = 0; x < kBlockTiles - 1; ++x) emit(x); // a walk shorter than three steps (or none) leaves some
         // This block's K/V rows and column layout are dead: the next block's loads go out now (see BlockLoads).
-        if (index + members < group_blocks) issue(block_at(index + members), ld);
+        const bool last_block = index + members >= group_blocks;
+        if (!last_block) issue(block_at(index + members), ld);
         if (nsteps > 0) {
-            // Query tiles still in flight after the walk: only waves 1..3 reached them.
-    #pragma unroll
-            for (int x = 0; x < kBlockTiles - 1; ++x) flush(base + nsteps + x);
+            // Query tiles still in flight after the walk (only waves 1..3 reached them): taken now, added during the
+            // next block's first steps (or now, after the last block).
+            tail_buf = qgbuf;
+#pragma unroll
+            for (int x = 0; x < kBlockTiles - 1; ++x) tail_tile[x] = take(base + nsteps + x, tail[x]) ? base + nsteps + x : -1;
+            if (last_block) {
+#pragma unroll
+                for (int x = 0; x < kBlockTiles - 1; ++x) emit(x);
+            }
         }
 
         // dK and dV of this wave's key tile (keys past the end fall outside the resources).
