@@ -419,6 +419,50 @@ def measure_reference_case(steps):
     return {k: (round(v, 6) if isinstance(v, float) else v) for k, v in timing.items()}
 
 
+PEAK_FP16_MFMA_TFLOPS = 2500.0  # MI355X dense FP16 matrix peak (AMD public specification; no sparsity)
+
+
+def measure_generic(cfg, steps):
+    """attention_generic_forward (AttentionGeneric.hip) on the config's Q, K, V and radius with fp32 and
+    fp16 storage. The generic entry point has no causal flag, so every (query, key) pair inside the radius window is
+    visited. fp32 storage runs the FP32 MFMA kernel; fp16 storage runs v_mfma_f32_32x32x16_f16, whose matrix work per
+    tile is 1/16 of the FP32 kernel's, so it is bound by the softmax VALU work (exp, max, sum: about 62 operations
+    and 16 exponentials per 32 x 32 tile and wave) rather than by the FP16 matrix peak it is reported against."""
+    import torch
+
+    from rocmkernels_amd import attention
+
+    device = torch.device("cuda:0")
+    q32, k32, v32, _, _, _ = make_inputs(cfg, device)
+    batch, heads, length, width = q32.shape
+    mask = torch.ones((batch, length), dtype=torch.uint8, device=device)
+    radius = cfg["radius"]
+    if radius < 0:
+        pairs = batch * heads * length * length
+    else:
+        per_query = [min(length - 1, i + radius) - max(0, i - radius) + 1 for i in range(length)]
+        pairs = batch * heads * sum(per_query)
+    flops = 4.0 * width * pairs
+    out = {}
+    for name, dtype, peak in (("f32", torch.float32, PEAK_FP32_MFMA_TFLOPS), ("f16", torch.float16, PEAK_FP16_MFMA_TFLOPS)):
+        q, k, v = (t.to(dtype) for t in (q32, k32, v32))
+        o = torch.empty_like(q)
+        lse = torch.empty((batch, heads, length, 2), device=device)
+
+        def launch():
+            attention.generic_forward(q, k, v, mask, radius=radius, output=o, lse=lse)
+
+        launch()
+        timing = time_samples(launch, [o, lse], steps)
+        tflops = flops / (timing["ms_per_launch"] * 1e-3) / 1e12
+        out[name] = {"ms_per_launch": round(timing["ms_per_launch"], 6), "ms_min": round(timing["ms_min"], 6),
+                     "ms_p95": round(timing["ms_p95"], 6), "tflops_visited": round(tflops, 4), "peak_tflops": peak,
+                     "frac_of_mfma_peak": round(tflops / peak, 4)}
+    out["workload"] = (f"generic forward: B{batch} x H{heads} x L{length} x d{width}, radius {radius}, not causal "
+                       f"(the generic entry point has no causal flag), {pairs} visited pairs")
+    return out
+
+
 def rounded(d):
     return {k: (round(v, 6) if isinstance(v, float) else v) for k, v in d.items()}
 
@@ -498,6 +542,7 @@ def main():
             result[part] = rounded(measured[part])
             result[part]["traffic"] = backward_traffic(args.config, part)
     result["rotary"] = measure_rotary(cfg, args.steps, args.warmup)
+    result["generic_forward"] = measure_generic(cfg, args.steps)
     if args.config == 2:
         result["reference_bench_case"] = measure_reference_case(args.steps)
     result["cpu_baseline"] = cpu_baseline(args.config, args.cpu_seconds) if args.cpu_seconds > 0 else None
