@@ -456,12 +456,15 @@ def test_fused_backward_config3_and_masked_batch(device):
     assert np.array_equal(delta.view(np.int32), ddelta.view(np.int32))
 
 
-@pytest.mark.parametrize("width,batch,length,radius", [(32, 64, 2048, -1), (64, 32, 4096, -1), (64, 16, 8192, 256)])
+@pytest.mark.parametrize("width,batch,length,radius", [(32, 64, 2048, -1), (64, 32, 4096, -1), (64, 16, 8192, 256),
+                                                       (32, 16, 4096, 100), (64, 12, 4096, 77)])
 def test_fused_backward_dispatch_order_subset(device, width, batch, length, radius):
     # 64 x 2048 causal at d=32 and 32 x 4096 at d=64: more key blocks (1024) than the piece table holds, so one workgroup
-    # per whole block in dispatch order, every dK/dV stored. Config 5 (radius 256): the band kernel, one workgroup per CU
-    # over whole key blocks. Checked on two sequences against the oracle, and the whole batch against the deterministic
-    # backward.
+    # per whole block in dispatch order, every dK/dV stored. Radius windows: the band kernel, one workgroup per CU over
+    # whole key blocks, so with more blocks than CUs every workgroup walks several and each block's loads and the
+    # previous walk's last dQ tiles cross the block transitions (config 5; 512 blocks at d=32; 384 blocks of 12
+    # sequences, which do not split over the 8 XCDs). Checked on two sequences against the oracle, and the whole batch
+    # against the deterministic backward.
     q, k, v, du = normal_case(960 + width, width, batch, 1, length, length)
     mask = np.ones((batch, length), np.uint8)
     mask[1, length // 3:] = 0
