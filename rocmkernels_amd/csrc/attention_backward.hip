@@ -108,10 +108,10 @@ __global__ __launch_bounds__(kWave * (NI > 0 ? NI * SPLIT : kWaves)) void attent
         const Buffer obuf = make_buffer(sequence(o, w.b, w.head), sequence_bytes(s.queries, o.st, D));
         float orow[HALF];
         buffer_load_span<VEC>(orow, obuf, qvalid ? static_cast<uint32_t>(query) * (4u * o.st) + 4u * h * HALF : kNoRow);
-        dlt = 0.0f;
+        float part[HALF / 4];
 #pragma unroll
-        for (int c = 0; c < HALF; ++c) dlt = fmaf(dor[c], orow[c], dlt);
-        dlt = halves_sum(dlt);
+        for (int i = 0; i < HALF / 4; ++i) part[i] = group_dot(dor + 4 * i, orow + 4 * i);
+        dlt = halves_sum(group_tree(part));
         if (w.sub == 0 && h == 0 && qvalid) delta[row] = dlt;
         if constexpr (MODE == kDeltaZeroDq) {
             // The fused dK/dV/dQ kernel accumulates into dQ: start every row of this tile at zero.

@@ -466,43 +466,44 @@ __global__ __launch_bounds__(kWave * kBlockTiles * STREAMS) void attention_fused
 }
 
 // δ = Σ dO·O per query row, dQ = 0, and dK = dV = 0 on the key blocks that the plan splits (those that see more than
-// `split_above` query tiles; their pieces add into dK/dV). Threads 0 .. 2·qrows - 1 compute δ, two lanes per row: lane h
-// runs the FMA chain over features h·D/2 .. h·D/2 + D/2 - 1 in order, as each half-wave of the deterministic backward
-// does, and the two halves are added, so δ is bit-identical to that path's. Every thread also clears one 16-byte group
-// of a dQ row and of a dK/dV row: D/4 times more waves than one row per lane pair (192 workgroups at 24 x 1024, fewer
-// than the CUs), which keeps enough stores in flight.
+// `split_above` query tiles; their pieces add into dK/dV). Each thread takes one 16-byte group of a row: the D/4 lanes
+// of a query row form δ with group_dot and the pairwise tree (shuffles at distance 1, 2, 4, ..., the same order as
+// the deterministic backward's lane-local tree, so δ is bit-identical to that path's), and each thread clears its group
+// of the dQ row and of the dK/dV row. Spreading δ over D/4 lanes per row keeps the loads of every workgroup in flight
+// at once (two lanes per row left 576 of the 768 workgroups at 24 x 1024 with nothing to load).
 template<int D>
 __global__ __launch_bounds__(256) void attention_fused_prepass_kernel(const Tensor o, const Tensor du, float *__restrict__ delta,
         float *__restrict__ dq, float *__restrict__ dk, float *__restrict__ dv, const Shape s, const int64_t qrows,
         const int64_t krows, const int split_above) {
-    constexpr int HALF = D / 2;
-    constexpr int G = D / 4; // 16-byte groups per row
+    constexpr int G = D / 4; // 16-byte groups per row: a power of two dividing the wave
     const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     const f32x4 zero{0.0f, 0.0f, 0.0f, 0.0f};
-    if (t < 2 * qrows) { // both lanes of a row pair are inside or outside
-        const int64_t r = t >> 1;
-        const int half = static_cast<int>(t & 1);
-        const int64_t seq = r / s.queries;
-        const int query = static_cast<int>(r - seq * s.queries);
+    if (t < qrows * G) { // the G lanes of a row are all inside or all outside
+        const int64_t r = t / G;
+        const int g = static_cast<int>(t & (G - 1));
+        // Sequence and query of the row; 32-bit arithmetic whenever the rows fit (always, short of 2^32 rows).
+        int64_t seq;
+        int query;
+        if (qrows <= 0xffffffffLL) {
+            const uint32_t r32 = static_cast<uint32_t>(r), nq = static_cast<uint32_t>(s.queries);
+            seq = r32 / nq;
+            query = static_cast<int>(r32 - static_cast<uint32_t>(seq) * nq);
+        } else {
+            seq = r / s.queries;
+            query = static_cast<int>(r - seq * s.queries);
+        }
         const int b = static_cast<int>(seq / s.heads), head = static_cast<int>(seq - static_cast<int64_t>(b) * s.heads);
-        const float *orow = o.data + static_cast<int64_t>(b) * o.sb + static_cast<int64_t>(head) * o.sh + static_cast<int64_t>(query) * o.st + half * HALF;
-        const float *urow = du.data + static_cast<int64_t>(b) * du.sb + static_cast<int64_t>(head) * du.sh + static_cast<int64_t>(query) * du.st + half * HALF;
-        f32x4 x[HALF / 4], y[HALF / 4];
+        const float *orow = o.data + static_cast<int64_t>(b) * o.sb + static_cast<int64_t>(head) * o.sh + static_cast<int64_t>(query) * o.st + 4 * g;
+        const float *urow = du.data + static_cast<int64_t>(b) * du.sb + static_cast<int64_t>(head) * du.sh + static_cast<int64_t>(query) * du.st + 4 * g;
+        const f32x4 x = *reinterpret_cast<const f32x4 *>(urow);
+        const f32x4 y = *reinterpret_cast<const f32x4 *>(orow);
+        const float xs[4] = {x[0], x[1], x[2], x[3]}, ys[4] = {y[0], y[1], y[2], y[3]};
+        float part = group_dot(xs, ys);
 #pragma unroll
-        for (int c = 0; c < HALF / 4; ++c) {
-            x[c] = *reinterpret_cast<const f32x4 *>(urow + 4 * c);
-            y[c] = *reinterpret_cast<const f32x4 *>(orow + 4 * c);
-        }
-        float part = 0.0f;
-#pragma unroll
-        for (int c = 0; c < HALF / 4; ++c) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) part = fmaf(x[c][e], y[c][e], part);
-        }
-        const float other = __shfl_xor(part, 1);
-        if (half == 0) delta[r] = part + other;
+        for (int m = 1; m < G; m <<= 1) part += __shfl_xor(part, m);
+        if (g == 0) delta[r] = part;
+        reinterpret_cast<f32x4 *>(dq)[t] = zero;
     }
-    if (t < qrows * G) reinterpret_cast<f32x4 *>(dq)[t] = zero;
     if (t < krows * G) {
         const int64_t r = t / G;
         // Key index within its sequence; 32-bit arithmetic whenever the key rows fit (always, short of 2^32 rows).
@@ -556,7 +557,7 @@ hipError_t launch(const BackwardArgs &a, const int cus, hipStream_t stream) {
     const int64_t rows = qrows > krows ? qrows : krows;
     // Blocks above the plan's piece length are split (no block is without a plan).
     const int split_above = planned && cp.plan.partial ? cp.plan.chunk : 0x7fffffff;
-    const int64_t threads_pre = (2 * qrows > rows * (D / 4)) ? 2 * qrows : rows * (D / 4);
+    const int64_t threads_pre = rows * (D / 4);
     hipLaunchKernelGGL((attention_fused_prepass_kernel<D>), dim3(static_cast<unsigned>((threads_pre + 255) / 256)), dim3(256), 0, stream,
             tensor(a.output, a.os), tensor(a.upstream, a.us), a.delta, a.gradient_q, a.gradient_k, a.gradient_v, shape, qrows, krows,
             split_above);
@@ -588,8 +589,7 @@ hipError_t launch_backward_prepass(const int D, const BackwardArgs &a, hipStream
     const Shape shape{a.batch, a.heads, a.queries, a.keys, a.radius, a.causal};
     const long long seqs = static_cast<long long>(a.batch) * a.heads;
     const int64_t qrows = seqs * a.queries;
-    const int G = D / 4;
-    const int64_t threads = (2 * qrows > qrows * G) ? 2 * qrows : qrows * G; // dQ rows and delta; dK/dV are left alone
+    const int64_t threads = qrows * (D / 4); // dQ rows and delta; dK/dV are left alone
     const unsigned grid = static_cast<unsigned>((threads + 255) / 256);
     if (D == 32) {
         hipLaunchKernelGGL((attention_fused_prepass_kernel<32>), dim3(grid), dim3(256), 0, stream, tensor(a.output, a.os),

@@ -65,6 +65,27 @@ __device__ __forceinline__ float halves_sum(const float x) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// δ = Σ dO·O of a row is summed in one fixed order by every kernel that forms it, so all backward paths write the
+// same bits: each 4-feature group is a product followed by an FMA chain (group_dot), and the groups are added as a
+// pairwise tree (groups 2i and 2i + 1, then adjacent pairs, and so on up to the two half rows).
+__device__ __forceinline__ float group_dot(const float *x, const float *y) {
+    float p = x[0] * y[0];
+    p = fmaf(x[1], y[1], p);
+    p = fmaf(x[2], y[2], p);
+    return fmaf(x[3], y[3], p);
+}
+
+// The tree over N consecutive groups held by one lane (N a power of two).
+template<int N>
+__device__ __forceinline__ float group_tree(float (&p)[N]) {
+#pragma unroll
+    for (int m = 1; m < N; m <<= 1) {
+#pragma unroll
+        for (int i = 0; i < N; i += 2 * m) p[i] += p[i + m];
+    }
+    return p[0];
+}
+
 // Bits lo..hi (inclusive, clamped to 0..31) set; 0 when the range is empty.
 __device__ __forceinline__ uint32_t bit_range(const int lo, const int hi) {
     const int a = min(max(lo, 0), 32);
