@@ -10,7 +10,9 @@
 //   * For Oᵀ the MFMA's 16-long reduction index is mapped onto the Sᵀ accumulator layout: MFMA u takes from lane
 //     (query, h) the probabilities held in accumulator registers 8u .. 8u + 7, i.e. keys tile_row(8u + j, h), so
 //     P is converted to fp16 in place (4 v_cvt_pk_f16_f32) and never leaves the lane; the Vᵀ operand of the same
-//     lane (feature, h) holds V[tile_row(8u + j, h)][feature].
+//     lane (feature, h) holds V[tile_row(8u + j, h)][feature]. With 16-byte aligned V rows (d = 32, 64) a tile's V
+//     rows arrive as 128-bit loads, pass through the wave's LDS slot and come back in that operand layout through
+//     ds_read_b64_tr_b16 (a transposing 16-bit LDS read, two per MFMA); otherwise each element is a 16-bit load.
 //   * The online softmax (lazy re-basing, exp2 with the scale folded into one FMA), the masks, the work mapping and
 //     the merge of the waves sharing a query tile follow attention_forward.hip.
 #include "attention_device.hpp"
@@ -51,13 +53,38 @@ __device__ __forceinline__ f16x8 load8h(const Buffer b, const uint32_t voffset) 
     }
 }
 
-template<int D, bool VEC, int SPLIT>
+// Row stride (halves) of a wave's staged V tile: rows are unpadded (padded strides that put the four rows of one
+// transposing read on distinct banks measured no faster).
+template<int D>
+constexpr int kVStride = D;
+
+// Operand of Oᵀ MFMA (t2, u) from the staged tile: lane (col, h) gets V[tile_row(8u + j, h)][32 t2 + col], j = 0..7,
+// as two transposing reads of 4 rows each. In each 16-lane group, lane L points at row r0 + L / 4, features
+// f0 + 4 (L mod 4) .. +3, and receives feature f0 + L of rows r0 .. r0 + 3 (r0 = 16u + 8p + 4h, f0 = 32 t2 + 16 (col / 16)).
+template<int D, int T2, int U>
+__device__ __forceinline__ f16x8 read_v_operand(const _Float16 *slot, const int lane_off) {
+    typedef __fp16 v4h __attribute__((ext_vector_type(4))); // the builtin's element type
+    const _Float16 *p = slot + lane_off + 16 * U * kVStride<D> + 32 * T2;
+    const f16x4 lo = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) v4h *)(p)));
+    const f16x4 hi = __builtin_bit_cast(f16x4,
+            __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) v4h *)(p + 8 * kVStride<D>)));
+    return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// STAGE_V (d = 32 or 64, 16-byte aligned V rows): a tile's V rows arrive with 128-bit loads and pass through the wave's
+// LDS slot, read back by transposing LDS reads into the Vᵀ operand layout (2 per MFMA) instead of one 16-bit load per
+// operand element (16·D/32 per lane and tile).
+template<int D, bool VEC, int SPLIT, bool STAGE_V>
 __global__ __launch_bounds__(kThreads) void attention_forward_f16_kernel(const TensorH q, const TensorH k, const TensorH v,
         const uint8_t *__restrict__ mask, _Float16 *__restrict__ out, const int osb, const int osh, const int ost,
         float *__restrict__ lse, const Shape s, const float scale) {
     constexpr int KC = D / 16;            // 16-feature chunks of a row: MFMAs per Sᵀ tile
     constexpr int DT = (D + 31) / 32;     // 32-feature slices of the output
     constexpr int ROWS = D < 32 ? D : 32; // valid features per slice
+    static_assert(!STAGE_V || (VEC && D >= 32), "staged V needs 128-bit rows of at least 32 features");
+    constexpr int VLOADS = STAGE_V ? D / 16 : 1; // 128-bit loads per lane for a 32-row V tile
+    constexpr int VCPR = D / 8;                  // 16-byte chunks per V row
+    constexpr int VRPL = kWave / VCPR;           // V rows per 128-bit load
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave); // wave-uniform: keeps tile bookkeeping scalar
@@ -111,26 +138,55 @@ __global__ __launch_bounds__(kThreads) void attention_forward_f16_kernel(const T
 
     struct Tile {
         f16x8 k[KC];
-        f16x8 v[DT][2];
+        f16x8 v[STAGE_V ? 1 : DT][2];
+        u32x4 vraw[VLOADS]; // STAGE_V: rows VRPL·i + lane / VCPR, 16-byte chunk lane mod VCPR
         int mask;
     };
+    // STAGE_V: this wave's V slot, and the lane's offsets into it for the 128-bit row writes and the transposing reads.
+    __shared__ __align__(16) _Float16 vslots[STAGE_V ? kWaves : 1][STAGE_V ? kTile * kVStride<D> : 1];
+    _Float16 *const vslot = vslots[STAGE_V ? wave : 0];
+    const int vrow = lane / VCPR; // row of the lane's chunk within each group of VRPL rows
+    const int vwrite = vrow * kVStride<D> + 8 * (lane % VCPR);
+    const int vread = (4 * h + ((lane & 15) >> 2)) * kVStride<D> + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
     auto load_tile = [&](Tile &t, const int key0) __attribute__((always_inline)) {
         const uint32_t key = static_cast<uint32_t>(key0 + col);
         t.mask = buffer_load_byte(mbuf, key);
 #pragma unroll
         for (int i = 0; i < KC; ++i) t.k[i] = load8h<VEC>(kbuf, key * kstep + 2u * (16 * i + 8 * h));
-        // V[key0 + tile_row(8u + j, h)][32 t2 + col]; lanes past a 16-wide head's last feature read 0.
-        const uint32_t vlane = col < ROWS ? static_cast<uint32_t>(key0 + 4 * h) * vstep + 2u * col : kNoRow;
+        if constexpr (STAGE_V) {
+            // Rows past the sequence read 0 through the range check (offsets wrap past it for key0 < 0).
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+            for (int i = 0; i < VLOADS; ++i)
+                t.vraw[i] = __builtin_amdgcn_raw_buffer_load_b128(vbuf, static_cast<int>(static_cast<uint32_t>(key0 + VRPL * i + vrow) * vstep +
+                        16u * static_cast<uint32_t>(lane % VCPR)), 0, 0);
+        } else {
+            // V[key0 + tile_row(8u + j, h)][32 t2 + col]; lanes past a 16-wide head's last feature read 0.
+            const uint32_t vlane = col < ROWS ? static_cast<uint32_t>(key0 + 4 * h) * vstep + 2u * col : kNoRow;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const uint32_t row = static_cast<uint32_t>(16 * u + 8 * (j >> 2) + (j & 3));
+            for (int u = 0; u < 2; ++u) {
 #pragma unroll
-                for (int t2 = 0; t2 < DT; ++t2)
-                    t.v[t2][u][j] = __builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(vbuf,
-                            static_cast<int>(vlane + 64u * t2), static_cast<int>(row * vstep), 0));
+                for (int j = 0; j < 8; ++j) {
+                    const uint32_t row = static_cast<uint32_t>(16 * u + 8 * (j >> 2) + (j & 3));
+#pragma unroll
+                    for (int t2 = 0; t2 < DT; ++t2)
+                        t.v[t2][u][j] = __builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(vbuf,
+                                static_cast<int>(vlane + 64u * t2), static_cast<int>(row * vstep), 0));
+                }
             }
+        }
+    };
+    // STAGE_V: the tile's V rows into the slot, rows of masked keys as zeros (they contribute exactly nothing, whatever
+    // their stored values hold). The previous tile's reads of the slot are complete first.
+    auto stage_v = [&](const Tile &t, const uint32_t bits) __attribute__((always_inline)) {
+        wave_lds_sync();
+#pragma unroll
+        for (int i = 0; i < VLOADS; ++i) {
+            u32x4 x = t.vraw[i];
+            if (bits != 0xffffffffu) {
+                const bool kept = (bits >> (VRPL * i + vrow)) & 1u;
+                x = kept ? x : u32x4{0u, 0u, 0u, 0u};
+            }
+            *reinterpret_cast<u32x4 *>(vslot + vwrite + VRPL * i * kVStride<D>) = x;
         }
     };
 
@@ -145,22 +201,37 @@ __global__ __launch_bounds__(kThreads) void attention_forward_f16_kernel(const T
         for (int i = 0; i < KC; ++i) sc = mfma16(t.k[i], qr[i], sc);
         __builtin_amdgcn_sched_barrier(0);
         load_tile(next, next_key0);
+        // STAGE_V: the tile's V rows go through the slot now, and the operand reads are issued before the softmax,
+        // whose VALU work covers their LDS round trip.
+        f16x8 vop[DT][2];
+        if constexpr (STAGE_V) {
+            stage_v(t, bits);
+            wave_lds_sync(); // the slot's rows are written
+            vop[0][0] = read_v_operand<D, 0, 0>(vslot, vread);
+            vop[0][1] = read_v_operand<D, 0, 1>(vslot, vread);
+            if constexpr (DT > 1) {
+                vop[DT - 1][0] = read_v_operand<D, DT - 1, 0>(vslot, vread);
+                vop[DT - 1][1] = read_v_operand<D, DT - 1, 1>(vslot, vread);
+            }
+        }
         __builtin_amdgcn_sched_barrier(0);
 
         if (bits != 0xffffffffu || !tile_in_window(s, q0, key0)) {
             const uint32_t visible = (bits & bit_range(wlo - key0, whi - key0)) >> (4 * h);
 #pragma unroll
             for (int j = 0; j < 16; ++j) sc[j] = (visible >> (8 * (j >> 2) + (j & 3))) & 1u ? sc[j] : -INFINITY;
-            if (bits != 0xffffffffu) {
-                // Masked keys contribute exactly nothing, whatever their stored values hold.
-                const uint32_t kept = bits >> (4 * h);
+            if constexpr (!STAGE_V) { // (staged rows were zeroed by stage_v)
+                if (bits != 0xffffffffu) {
+                    // Masked keys contribute exactly nothing, whatever their stored values hold.
+                    const uint32_t kept = bits >> (4 * h);
 #pragma unroll
-                for (int u = 0; u < 2; ++u) {
+                    for (int u = 0; u < 2; ++u) {
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const bool ok = (kept >> (16 * u + 8 * (j >> 2) + (j & 3))) & 1u;
+                        for (int j = 0; j < 8; ++j) {
+                            const bool ok = (kept >> (16 * u + 8 * (j >> 2) + (j & 3))) & 1u;
 #pragma unroll
-                        for (int t2 = 0; t2 < DT; ++t2) t.v[t2][u][j] = ok ? t.v[t2][u][j] : static_cast<_Float16>(0.0f);
+                            for (int t2 = 0; t2 < DT; ++t2) t.v[t2][u][j] = ok ? t.v[t2][u][j] : static_cast<_Float16>(0.0f);
+                        }
                     }
                 }
             }
@@ -188,7 +259,10 @@ __global__ __launch_bounds__(kThreads) void attention_forward_f16_kernel(const T
                     p[j + 1] = pair[1];
                 }
 #pragma unroll
-                for (int t2 = 0; t2 < DT; ++t2) o[t2] = mfma16(t.v[t2][u], p, o[t2]);
+                for (int t2 = 0; t2 < DT; ++t2) {
+                    if constexpr (STAGE_V) o[t2] = mfma16(vop[t2][u], p, o[t2]);
+                    else o[t2] = mfma16(t.v[t2][u], p, o[t2]);
+                }
             }
         };
         if (__builtin_expect(__ballot(m_half > m_lazy) == 0, 1)) {
@@ -308,11 +382,11 @@ TensorH tensor_h(const void *p, const rocmkernels_strides &s) {
     return TensorH{static_cast<const _Float16 *>(p), s.batch, s.head, s.token};
 }
 
-template<int D, bool VEC, int SPLIT>
+template<int D, bool VEC, int SPLIT, bool STAGE_V>
 void launch(const HalfForwardArgs &a, const int64_t items, hipStream_t stream) {
     const Shape shape{a.batch, a.heads, a.queries, a.keys, a.radius, 0};
     const float scale = 1.0f / sqrtf(static_cast<float>(D));
-    hipLaunchKernelGGL((attention_forward_f16_kernel<D, VEC, SPLIT>), dim3(workgroups_for(items, SPLIT)), dim3(kThreads), 0, stream,
+    hipLaunchKernelGGL((attention_forward_f16_kernel<D, VEC, SPLIT, STAGE_V>), dim3(workgroups_for(items, SPLIT)), dim3(kThreads), 0, stream,
             tensor_h(a.q, a.qs), tensor_h(a.k, a.ks), tensor_h(a.v, a.vs), reinterpret_cast<const uint8_t *>(a.mask),
             static_cast<_Float16 *>(a.output), a.os.batch, a.os.head, a.os.token, a.lse, shape, scale);
 }
@@ -322,12 +396,20 @@ void dispatch(const HalfForwardArgs &a, const int64_t items, hipStream_t stream)
     // 128-bit row loads need 16-byte aligned rows; the output's 4-half stores 8-byte alignment.
     const bool vec = aligned16(a.q) && aligned16(a.k) && strides8(a.qs) && strides8(a.ks) && aligned8(a.output) && strides4(a.os);
     const int split = forward_split_for(items);
-    if (vec) {
-        if (split == 1) launch<D, true, 1>(a, items, stream);
-        else launch<D, true, 4>(a, items, stream);
+    // V rows staged through LDS need 16-byte aligned rows too (d = 32 and 64).
+    bool stage = false;
+    if constexpr (D >= 32) stage = vec && aligned16(a.v) && strides8(a.vs);
+    if (stage) {
+        if constexpr (D >= 32) {
+            if (split == 1) launch<D, true, 1, true>(a, items, stream);
+            else launch<D, true, 4, true>(a, items, stream);
+        }
+    } else if (vec) {
+        if (split == 1) launch<D, true, 1, false>(a, items, stream);
+        else launch<D, true, 4, false>(a, items, stream);
     } else {
-        if (split == 1) launch<D, false, 1>(a, items, stream);
-        else launch<D, false, 4>(a, items, stream);
+        if (split == 1) launch<D, false, 1, false>(a, items, stream);
+        else launch<D, false, 4, false>(a, items, stream);
     }
 }
 

@@ -129,3 +129,38 @@ def test_generic_fully_masked_batch(device):
     assert np.all(lse[1, ..., 0] == -np.inf) and np.all(lse[1, ..., 1] == 0.0)
     want = oracle.attention(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32), mask)
     check(out, lse, want, "f16", "masked batch")
+
+
+@pytest.mark.parametrize("width", [16, 32, 64])
+def test_generic_fp16_masked_keys_with_garbage_values_are_ignored(device, width):
+    # Masked keys contribute exactly nothing whatever their rows hold: the staged V path (d = 32, 64) writes zeros
+    # for their rows, the 16-bit path zeroes their operand elements. The masked keys sit inside and at the end of
+    # tiles, in every query tile's key range.
+    batch, heads, queries, keys = 2, 2, 96, 100
+    q, k, v = (inputs.normal(70 + i, (batch, heads, n, width)).astype(np.float16) for i, n in enumerate((queries, keys, keys)))
+    mask = np.ones((batch, keys), np.uint8)
+    mask[0, 40:48] = 0
+    mask[0, 90:] = 0
+    mask[1, 5] = 0
+    want = oracle.attention(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32), mask)
+    hidden = mask[:, None, :, None] == 0
+    k = np.where(hidden, np.float16(np.inf), k)
+    v = np.where(hidden, np.float16(np.nan), v)
+    out, lse = run(device, q, k, v, mask)
+    check(out, lse, want, "f16", f"d{width} garbage in masked rows")
+
+
+@pytest.mark.parametrize("width", [32, 64])
+def test_generic_fp16_one_wave_per_item(device, width):
+    # 8192 query tiles (one wave per item, forward_split_for) with a radius window; odd key count so the last tile is
+    # partial and its missing rows come from the range check.
+    batch, heads, queries, keys = 8, 32, 1024, 1023
+    seed = 800 + width
+    q = inputs.normal(seed, (batch, heads, queries, width)).astype(np.float16)
+    k = inputs.normal(seed + 1, (batch, heads, keys, width)).astype(np.float16)
+    v = inputs.normal(seed + 2, (batch, heads, keys, width)).astype(np.float16)
+    mask = np.ones((batch, keys), np.uint8)
+    mask[3, 500:] = 0
+    want = oracle.attention(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32), mask, radius=40)
+    out, lse = run(device, q, k, v, mask, radius=40)
+    check(out, lse, want, "f16", f"d{width} 8192 items")
