@@ -423,9 +423,9 @@ PEAK_FP16_MFMA_TFLOPS = 2500.0  # MI355X dense FP16 matrix peak (AMD public spec
 
 
 def measure_generic(cfg, steps):
-    """attention_generic_forward (AttentionGeneric.hip) on the config's Q, K, V and radius with fp32 and
-    fp16 storage. The generic entry point has no causal flag, so every (query, key) pair inside the radius window is
-    visited. fp32 storage runs the FP32 MFMA kernel; fp16 storage runs v_mfma_f32_32x32x16_f16, whose matrix work per
+    """attention_generic_forward (the reference's Generic/Attention/AttentionGeneric.hip:36-309) on the config's Q, K,
+    V and radius with fp32 and fp16 storage. The generic entry point has no causal flag, so every (query, key) pair
+    inside the radius window is visited. fp32 storage runs the FP32 MFMA kernel; fp16 storage runs v_mfma_f32_32x32x16_f16, whose matrix work per
     tile is 1/16 of the FP32 kernel's, so it is bound by the softmax VALU work (exp, max, sum: about 62 operations
     and 16 exponentials per 32 x 32 tile and wave) rather than by the FP16 matrix peak it is reported against."""
     import torch
