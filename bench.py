@@ -83,7 +83,7 @@ def make_inputs(cfg, device):
     return q, k, v, du, mask, lengths
 
 
-SETTLE_SECONDS = 0.25
+SETTLE_SECONDS = 1.0    # untimed load before each timed region (the clock settles within about 20 ms)
 SAMPLES_MIN = 20       # timed samples per measurement (the reference harness records at least 20)
 SAMPLE_MS = 10.0       # each sample is a graph of back-to-back launches lasting at least this long
 FLUSH_MIB = 512        # written before every sample: larger than the 256 MB Infinity Cache plus the 8 x 4 MB L2s
