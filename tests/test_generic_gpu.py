@@ -164,3 +164,20 @@ def test_generic_fp16_one_wave_per_item(device, width):
     want = oracle.attention(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32), mask, radius=40)
     out, lse = run(device, q, k, v, mask, radius=40)
     check(out, lse, want, "f16", f"d{width} 8192 items")
+
+
+@pytest.mark.parametrize("width", [32, 64])
+def test_generic_fp16_token_major_aligned(device, width):
+    # [B][T][H][D] storage viewed as [B][H][T][D]: token stride H*D halves, rows 16-byte aligned, so K and V take
+    # the 128-bit paths (V staged through LDS) with a row step other than the head width.
+    batch, heads, queries, keys = 2, 3, 130, 97
+    arrays = [inputs.normal(60 + i, (batch, n, heads, width)).astype(np.float16) for i, n in enumerate((queries, keys, keys))]
+    views = [torch.from_numpy(a).to(device).permute(0, 2, 1, 3) for a in arrays]
+    assert views[2].stride(2) == heads * width
+    mask = np.ones((batch, keys), np.uint8)
+    mask[1, 60:] = 0
+    tm = torch.from_numpy(mask).to(device)
+    out, lse = attention.generic_forward(*views, tm, radius=33)
+    torch.cuda.synchronize()
+    want = oracle.attention(*(a.transpose(0, 2, 1, 3).astype(np.float32) for a in arrays), mask, radius=33)
+    check(out.float().cpu().numpy(), lse.cpu().numpy(), want, "f16", f"d{width} token-major")
