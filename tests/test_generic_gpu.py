@@ -181,3 +181,18 @@ def test_generic_fp16_token_major_aligned(device, width):
     torch.cuda.synchronize()
     want = oracle.attention(*(a.transpose(0, 2, 1, 3).astype(np.float32) for a in arrays), mask, radius=33)
     check(out.float().cpu().numpy(), lse.cpu().numpy(), want, "f16", f"d{width} token-major")
+
+
+@pytest.mark.parametrize("batch,heads,length,width,radius", [
+    (2, 12, 1024, 32, -1),   # config 2's shape (no causal flag in this API: every pair)
+    (32, 1, 2048, 64, -1),   # config 4's
+    (16, 1, 8192, 64, 256),  # config 5's
+])
+def test_generic_fp16_benchmark_shapes(device, batch, heads, length, width, radius):
+    # The shapes bench.py times the generic forward on, in full, against the oracle on the fp16 inputs.
+    seed = 500 + width + length
+    q, k, v = (inputs.normal(seed + i, (batch, heads, length, width)).astype(np.float16) for i in range(3))
+    mask = np.ones((batch, length), np.uint8)
+    want = oracle.attention(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32), mask, radius=radius)
+    out, lse = run(device, q, k, v, mask, radius=radius)
+    check(out, lse, want, "f16", f"{batch}x{heads}x{length} d{width} r{radius}")
