@@ -24,8 +24,8 @@
 // of a split block adds its dK/dV into memory zeroed by the pre-pass, a whole block stores them. Without a plan (too
 // many pieces for the kernel-argument table), one workgroup per whole block, heaviest first, in dispatch order.
 //
-// A pre-pass kernel computes δ (bit-identical to the deterministic backward's: two half-row FMA chains, then their
-// sum) and zeroes dQ (and dK/dV when some block is split). dQ (and the dK/dV of split blocks) depend on the order in
+// A pre-pass kernel computes δ (bit-identical to the deterministic backward's: 4-feature partial products added in
+// the same pairwise tree, group_dot and group_tree) and zeroes dQ (and dK/dV when some block is split). dQ (and the dK/dV of split blocks) depend on the order in
 // which the atomics land, so their low bits vary from run to run.
 #include "attention_block_plan.hpp"
 #include "attention_device.hpp"
