@@ -196,3 +196,25 @@ def test_generic_fp16_benchmark_shapes(device, batch, heads, length, width, radi
     want = oracle.attention(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32), mask, radius=radius)
     out, lse = run(device, q, k, v, mask, radius=radius)
     check(out, lse, want, "f16", f"{batch}x{heads}x{length} d{width} r{radius}")
+
+
+@pytest.mark.parametrize("width", [32, 64])
+def test_generic_fp16_staged_v_is_bit_identical(device, width):
+    # The staged V path (128-bit loads, LDS, transposing reads) feeds the MFMAs the same operands as the 16-bit path:
+    # the same inputs with V as an unaligned view (16-bit loads) give the same bits, padding and radius included.
+    batch, heads, queries, keys = 2, 2, 150, 133
+    q, k, v = (inputs.normal(80 + i, (batch, heads, n, width)).astype(np.float16) for i, n in enumerate((queries, keys, keys)))
+    mask = np.ones((batch, keys), np.uint8)
+    mask[0, 100:] = 0
+    mask[1, 7] = 0
+    tq, tk, tv = (torch.from_numpy(a).to(device) for a in (q, k, v))
+    tm = torch.from_numpy(mask).to(device)
+    wide = torch.zeros(batch, heads, keys, width + 1, dtype=torch.float16, device=device)
+    wide[..., 1:] = tv
+    tv_unaligned = wide[..., 1:]
+    assert tv_unaligned.data_ptr() % 16 != 0
+    staged, staged_lse = attention.generic_forward(tq, tk, tv, tm, radius=40)
+    plain, plain_lse = attention.generic_forward(tq, tk, tv_unaligned, tm, radius=40)
+    torch.cuda.synchronize()
+    assert torch.equal(staged.view(torch.int16), plain.view(torch.int16))
+    assert torch.equal(staged_lse.view(torch.int32), plain_lse.view(torch.int32))
