@@ -154,11 +154,13 @@ __global__ __launch_bounds__(kThreads) void attention_forward_f16_kernel(const T
 #pragma unroll
         for (int i = 0; i < KC; ++i) t.k[i] = load8h<VEC>(kbuf, key * kstep + 2u * (16 * i + 8 * h));
         if constexpr (STAGE_V) {
-            // Rows past the sequence read 0 through the range check (offsets wrap past it for key0 < 0).
+            // Rows past the sequence read 0 through the range check.
+            const uint32_t chunk = 16u * static_cast<uint32_t>(lane % VCPR);
 #pragma unroll
-            for (int i = 0; i < VLOADS; ++i)
-                t.vraw[i] = __builtin_amdgcn_raw_buffer_load_b128(vbuf, static_cast<int>(static_cast<uint32_t>(key0 + VRPL * i + vrow) * vstep +
-                        16u * static_cast<uint32_t>(lane % VCPR)), 0, 0);
+            for (int i = 0; i < VLOADS; ++i) {
+                const uint32_t row = static_cast<uint32_t>(key0 + VRPL * i + vrow);
+                t.vraw[i] = __builtin_amdgcn_raw_buffer_load_b128(vbuf, static_cast<int>(row * vstep + chunk), 0, 0);
+            }
         } else {
             // V[key0 + tile_row(8u + j, h)][32 t2 + col]; lanes past a 16-wide head's last feature read 0.
             const uint32_t vlane = col < ROWS ? static_cast<uint32_t>(key0 + 4 * h) * vstep + 2u * col : kNoRow;
