@@ -393,25 +393,40 @@ void launch(const HalfForwardArgs &a, const int64_t items, hipStream_t stream) {
             static_cast<_Float16 *>(a.output), a.os.batch, a.os.head, a.os.token, a.lse, shape, scale);
 }
 
+// Waves per item: the fewest of 1, 2 and 4 that still give every SIMD its resident waves (two at d = 64, three at
+// d = 32, four at d = 16). An fp16 tile costs a fraction of an FP32 one, so a wave's start and the merge of an item's
+// waves weigh more here than in the FP32 kernel, whose own rule (forward_split_for) keeps more waves per item. Measured
+// on the generic fp16 forward: 32 x 2048 x 64 82.1 -> 76.7 µs and 16 x 8192 x 64 (radius 256) 65.5 -> 54.6 µs with one
+// wave per item; 24 x 2048 x 64 62.7 µs with two against 64.8 with four; 24 x 1024 x 32 keeps four (14.0 µs against
+// 14.7 with two and 17.6 with one).
+int f16_split_for(const int64_t items, const int D, const int cus) {
+    const int64_t slots = static_cast<int64_t>(cus) * kWaves * (D == 64 ? 2 : D == 32 ? 3 : 4);
+    if (items >= slots) return 1;
+    if (2 * items >= slots) return 2;
+    return 4;
+}
+
+template<int D, bool VEC, bool STAGE_V>
+void launch_split(const HalfForwardArgs &a, const int64_t items, const int split, hipStream_t stream) {
+    if (split == 1) launch<D, VEC, 1, STAGE_V>(a, items, stream);
+    else if (split == 2) launch<D, VEC, 2, STAGE_V>(a, items, stream);
+    else launch<D, VEC, 4, STAGE_V>(a, items, stream);
+}
+
 template<int D>
-void dispatch(const HalfForwardArgs &a, const int64_t items, hipStream_t stream) {
+void dispatch(const HalfForwardArgs &a, const int64_t items, const int cus, hipStream_t stream) {
     // 128-bit row loads need 16-byte aligned rows; the output's 4-half stores 8-byte alignment.
     const bool vec = aligned16(a.q) && aligned16(a.k) && strides8(a.qs) && strides8(a.ks) && aligned8(a.output) && strides4(a.os);
-    const int split = forward_split_for(items);
+    const int split = f16_split_for(items, D, cus);
     // V rows staged through LDS need 16-byte aligned rows too (d = 32 and 64).
     bool stage = false;
     if constexpr (D >= 32) stage = vec && aligned16(a.v) && strides8(a.vs);
     if (stage) {
-        if constexpr (D >= 32) {
-            if (split == 1) launch<D, true, 1, true>(a, items, stream);
-            else launch<D, true, 4, true>(a, items, stream);
-        }
+        if constexpr (D >= 32) launch_split<D, true, true>(a, items, split, stream);
     } else if (vec) {
-        if (split == 1) launch<D, true, 1, false>(a, items, stream);
-        else launch<D, true, 4, false>(a, items, stream);
+        launch_split<D, true, false>(a, items, split, stream);
     } else {
-        if (split == 1) launch<D, false, 1, false>(a, items, stream);
-        else launch<D, false, 4, false>(a, items, stream);
+        launch_split<D, false, false>(a, items, split, stream);
     }
 }
 
@@ -420,9 +435,12 @@ void dispatch(const HalfForwardArgs &a, const int64_t items, hipStream_t stream)
 hipError_t launch_forward_f16(const int D, const HalfForwardArgs &a, hipStream_t stream) {
     const int64_t items = static_cast<int64_t>((a.queries + kTile - 1) / kTile) * a.batch * a.heads;
     if (items > 0x7fffffff || !fits_h(a.queries, a.qs, D) || !fits_h(a.keys, a.ks, D) || !fits_h(a.keys, a.vs, D)) return hipErrorInvalidValue;
-    if (D == 16) dispatch<16>(a, items, stream);
-    else if (D == 32) dispatch<32>(a, items, stream);
-    else dispatch<64>(a, items, stream);
+    int cus = 0;
+    const hipError_t error = compute_units(cus);
+    if (error != hipSuccess) return error;
+    if (D == 16) dispatch<16>(a, items, cus, stream);
+    else if (D == 32) dispatch<32>(a, items, cus, stream);
+    else dispatch<64>(a, items, cus, stream);
     return hipGetLastError();
 }
 

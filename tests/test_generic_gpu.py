@@ -218,3 +218,19 @@ def test_generic_fp16_staged_v_is_bit_identical(device, width):
     torch.cuda.synchronize()
     assert torch.equal(staged.view(torch.int16), plain.view(torch.int16))
     assert torch.equal(staged_lse.view(torch.int32), plain_lse.view(torch.int32))
+
+
+@pytest.mark.parametrize("batch,heads,length,width,radius", [
+    (2, 12, 2048, 64, -1),   # 1536 query tiles at d = 64: two waves per item
+    (2, 16, 2048, 32, 300),  # 2048 at d = 32: two waves per item, radius window
+    (1, 64, 1024, 16, -1),   # 2048 at d = 16: two waves per item
+])
+def test_generic_fp16_two_waves_per_item(device, batch, heads, length, width, radius):
+    # Item counts between half and all of the resident wave slots take two waves per query tile (f16_split_for).
+    seed = 600 + width + length
+    q, k, v = (inputs.normal(seed + i, (batch, heads, length, width)).astype(np.float16) for i in range(3))
+    mask = np.ones((batch, length), np.uint8)
+    mask[-1, length // 3:] = 0
+    want = oracle.attention(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32), mask, radius=radius)
+    out, lse = run(device, q, k, v, mask, radius=radius)
+    check(out, lse, want, "f16", f"{batch}x{heads}x{length} d{width} r{radius}")
