@@ -457,7 +457,8 @@ def measure_generic(cfg, steps):
         tflops = flops / (timing["ms_per_launch"] * 1e-3) / 1e12
         out[name] = {"ms_per_launch": round(timing["ms_per_launch"], 6), "ms_min": round(timing["ms_min"], 6),
                      "ms_p95": round(timing["ms_p95"], 6), "tflops_visited": round(tflops, 4), "peak_tflops": peak,
-                     "frac_of_mfma_peak": round(tflops / peak, 4)}
+                     "frac_of_mfma_peak": round(tflops / peak, 4), "samples": timing["samples"],
+                     "launches_per_sample": timing["launches_per_sample"]}
     out["workload"] = (f"generic forward: B{batch} x H{heads} x L{length} x d{width}, radius {radius}, not causal "
                        f"(the generic entry point has no causal flag), {pairs} visited pairs")
     return out
