@@ -391,15 +391,18 @@ bool launch_planned(const ForwardArgs &a, const Plan &plan, hipStream_t stream) 
 }
 
 // Waves per item in dispatch order. Under a causal mask without a radius window item costs run from one tile to the
-// whole sequence, and more waves per item (forward_split_for) even out the SIMDs' loads: config 4 forward 145.5 µs
-// with four waves per item against 153.4 with two and 197.1 with one. Otherwise (no mask, or a radius window) items
-// cost about the same, and the fewest waves that still fill every SIMD's resident slots (two waves per SIMD at
-// d = 64, three at d <= 32) win, since a wave's start and the merge of an item's waves cost more than they balance:
-// config 5 forward 90.2 µs with one wave per item against 96.5 with two and 114.4 with four; without a mask, 32 x 2048
-// at d = 64 256.8 against 266.6 µs (four waves) and 16 x 8192 at d = 64, radius 256, 149.9 against 158.3 µs (two).
+// whole sequence, and more waves per item (forward_split_for) even out the SIMDs' loads: config 4 forward 145.5 µs with
+// four waves per item against 153.4 with two and 197.1 with one. Otherwise (no mask, or a radius window of at most a
+// quarter of the sequence) items cost about the same, and the fewest waves that still fill every SIMD's resident slots
+// (two waves per SIMD at d = 64, three at d <= 32) win, since a wave's start and the merge of an item's waves cost more
+// than they balance: config 5 forward 90.2 µs with one wave per item against 96.5 with two and 114.4 with four; without
+// a mask, 32 x 2048 at d = 64 256.8 against 266.6 µs (four waves) and 16 x 8192 at d = 64, radius 256, 149.9 against
+// 158.3 µs (two).
 template<int D>
 int dispatch_split(const ForwardArgs &a, const int64_t items, const int cus) {
-    if (a.causal && a.radius < 0) return forward_split_for(items);
+    // A radius window over more than a quarter of the sequence ramps item costs up over most of it.
+    const bool varied = (a.causal && a.radius < 0) || (a.radius >= 0 && 4LL * a.radius > a.queries);
+    if (varied) return forward_split_for(items);
     const int64_t slots = static_cast<int64_t>(cus) * kWaves * (D == 64 ? 2 : 3);
     return items >= slots ? 1 : 2 * items >= slots ? 2 : 4;
 }
