@@ -228,7 +228,7 @@ def backward(q, k, v, mask, output, lse, upstream, radius=-1, causal=False, entr
 
     A causal mask, ``entry="ex"``, ``fused`` or ``deterministic`` go through the *_ex entry points, whose default
     takes the faster backward for the call (the fused one, whose dQ is accumulated with atomics, for 128-bit aligned
-    inputs, except under a radius window at head width 32); ``fused`` asks for the fused backward, ``deterministic`` for the bit-reproducible two-kernel one. Otherwise
+    inputs); ``fused`` asks for the fused backward, ``deterministic`` for the bit-reproducible two-kernel one. Otherwise
     ``entry`` picks the reference entry point ("simple", "tiled", "tuned", "profile", "query_profile"), which always
     runs the deterministic kernels."""
     torch = _torch()

@@ -6,8 +6,8 @@ the ctypes binding).
 ``attention_fp32(q, k, v, mask, radius, causal)`` returns O = softmax(QKᵀ/√D + mask) V for q/k/v [B][H][L][D]
 float32 CUDA tensors (D = 32 or 64). The forward keeps O and the {max, sum} statistics; the backward runs the
 library's *_ex backward entry point on them: by default the faster backward for the call (the fused one, whose dQ is
-accumulated with atomics, for 128-bit aligned inputs except under a radius window at head width 32), with
-``deterministic=True`` the bit-reproducible two-kernel one.
+accumulated with atomics, for 128-bit aligned inputs), with ``deterministic=True`` the bit-reproducible two-kernel
+one.
 Everything runs on the GPU through the C ABI; there is no CPU path.
 """
 import torch

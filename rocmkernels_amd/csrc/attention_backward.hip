@@ -815,10 +815,11 @@ template<int D, bool VEC>
 hipError_t run(BackwardStage stage, const BackwardArgs &a, const int cus, hipStream_t stream) {
     const int64_t kitems = static_cast<int64_t>((a.keys + kTile - 1) / kTile) * a.batch * a.heads;
     // The fused key-block kernels need 128-bit access; without it the deterministic kernels measured faster.
-    // Auto takes the fused kernels wherever they exist (128-bit access) and measured faster: under a radius window at
-    // D = 32 the band kernel did not (16 sequences x 8192 tokens, radius 256, causal: 147 us against 146 us for the
-    // deterministic pair; at D = 64 277 us against 288 us).
-    if (stage == kBackwardAuto) stage = VEC && (a.radius < 0 || D == 64) ? kBackwardFused : kBackwardAll;
+    // Auto takes the fused kernels wherever they exist (128-bit access): under a radius window the band kernel against
+    // the deterministic pair, causal, measured 146.4 against 160.3 us at D = 32 (16 sequences x 8192 tokens, radius
+    // 256), 124.9 against 147.8 us (32 x 2048, radius 512), 101.9 against 103.4 us (32 x 4096, radius 128), and 258
+    // against 287 us at D = 64 (config 5).
+    if (stage == kBackwardAuto) stage = VEC ? kBackwardFused : kBackwardAll;
     if (stage == kBackwardFused) {
         // Key-block kernels (one dQ add per element per 128 keys): without a radius window the piece-planned one; under a
         // radius window the band kernel, whose skewed walk visits each key tile's own band only (the key-block walk over
