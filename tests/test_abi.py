@@ -205,3 +205,33 @@ def test_cmake_project_targets_gfx950_only():
     assert arches == {"gfx950"}
     assert "libROCmKernels.Kernels.a" in text and "libROCmKernels.Kernels.Shared.so" in text
     assert "nvcc" not in text and "cuda" not in text.lower().replace("--cuda-device-only", "")
+
+
+def test_reference_style_cpp_caller_compiles_and_links_common(tmp_path):
+    # A caller written as the reference's generic tests are (Generic/AttentionGenericTests.cpp:106-139): DeviceBuffer<__half>
+    # storage, AttentionGenericForward(..., DTypeOf<__half>::value) and QueryDevice, linked against the static kernel
+    # archive and ROCmKernels.Common (DeviceBuffer.hpp, Device.hpp, DType.hpp's DTypeOf). Without a GPU it checks the
+    # empty buffer, the wrapper's invalid-argument throw and that the device queries report the missing device.
+    lib_dir = os.path.dirname(attention.library_path())
+    binary = str(tmp_path / "common_consumer")
+    subprocess.run(["g++", "-std=c++17", "-Wall", "-Wextra", "-Werror", "-D__HIP_PLATFORM_AMD__", "-DCOMMON_CONSUMER_MAIN",
+                    f"-I{INCLUDE}", "-I/opt/rocm/include", os.path.join(ROOT, "tests", "cpp", "common_consumer.cpp"),
+                    os.path.join(lib_dir, "libROCmKernels.Kernels.a"), os.path.join(lib_dir, "libROCmKernels.Common.a"),
+                    "-o", binary, "-L/opt/rocm/lib", "-Wl,-rpath,/opt/rocm/lib", "-lamdhip64"],
+                   check=True, capture_output=True, text=True)
+    result = subprocess.run([binary], capture_output=True, text=True, timeout=60)
+    assert result.returncode == 0, result.stdout + result.stderr
+    assert "0 failure(s)" in result.stdout
+    assert "invalid argument" in result.stdout
+
+
+def test_kernel_targets_link_common_publicly():
+    # Both kernel targets carry ROCmKernels.Common to their consumers (the reference's CMakeLists.txt:120,133): the
+    # GPU consumer, linked against ROCmKernels.Kernels.Shared alone, gets libROCmKernels.Common.a on its link line.
+    with open(os.path.join(ROOT, "build", "build.ninja")) as handle:
+        text = handle.read()
+    links = [block for block in text.split("\nbuild ") if "librocmkernels_common_consumer.so" in block.split(":")[0]]
+    assert links and "libROCmKernels.Common.a" in links[0]
+    with open(os.path.join(ROOT, "CMakeLists.txt")) as handle:
+        cmake = handle.read()
+    assert "target_link_libraries(${target_name} PUBLIC ROCmKernels.Common" in cmake
