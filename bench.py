@@ -286,16 +286,24 @@ def cpu_baseline(config, seconds):
 
 
 def forward_kernel_name(cfg, cus):
-    """Name rocprofv3 reports for the forward kernel instance that runs on this config. Template arguments: head width,
-    statistics-only, 16-byte vector loads, waves per 32-query item and items per persistent workgroup (0: dispatch
-    order), chosen from the item count as rk::launch_mapped (rocmkernels_amd/csrc/attention_forward.hip) does."""
+    """Name rocprofv3 reports for the forward kernel instance that runs on this config (every config is causal).
+    Template arguments: head width, statistics-only, 16-byte vector loads, waves per 32-query item and items per
+    persistent workgroup (0: dispatch order), chosen as rk::launch_mapped and rk::dispatch_split
+    (rocmkernels_amd/csrc/attention_forward.hip) choose them."""
     items = (cfg["length"] + 31) // 32 * cfg["batch"] * cfg["heads"]
-    resident = 3 if cfg["width"] == 32 else 2
+    resident = 3 if cfg["width"] <= 32 else 2  # resident_items_per_cu
     if cus < items <= resident * cus:
         bins = min(items, cus)
         rounds = -(-items // bins)
         return f"rk::attention_forward_kernel<{cfg['width']}, false, true, 4, {3 if rounds == 3 else 2}>"
-    split = 1 if items >= 8192 else 2 if items >= 4096 else 4  # forward_split_for (attention_launch.hpp)
+    # dispatch_split: item costs vary (causal without a radius window, or a window wider than a quarter of the
+    # sequence): forward_split_for; otherwise the fewest waves per item that fill every SIMD's resident slots.
+    radius, length = cfg["radius"], cfg["length"]
+    if radius < 0 or 4 * radius > length:
+        split = 1 if items >= 8192 else 2 if items >= 4096 else 4  # forward_split_for (attention_launch.hpp)
+    else:
+        slots = cus * 4 * (2 if cfg["width"] == 64 else 3)
+        split = 1 if items >= slots else 2 if 2 * items >= slots else 4
     return f"rk::attention_forward_kernel<{cfg['width']}, false, true, {split}, 0>"
 
 
@@ -319,13 +327,12 @@ def load_traffic(kernel, config):
 
 def backward_traffic(config, part):
     """HBM and algorithmic bytes per launch of the kernels one backward call runs, from profiles/traffic.json: the fused
-    pre-pass and the fused (no radius window) or band kernel for the default backward where the library takes them
-    (128-bit access, which the bench inputs have, and no radius window at d=32: rk::run in attention_backward.hip), the
-    dQ and dK/dV kernels otherwise and for the deterministic backward."""
+    pre-pass and the fused (no radius window) or band kernel (radius window) for the default backward, which the library
+    takes for inputs with 128-bit access, as every bench input has (rk::run in attention_backward.hip); the dQ and
+    dK/dV kernels for the deterministic backward."""
     suffix = f" config{profile_config(config)}"
     rows = {k[:-len(suffix)]: v for k, v in traffic_table().items() if k.endswith(suffix) and "forward_kernel" not in k}
-    cfg = CONFIGS[config]
-    fused = part == "backward" and (cfg["radius"] < 0 or cfg["width"] == 64)
+    fused = part == "backward"
     names = sorted(n for n in rows if ("fused" in n or "band" in n) == fused)
     if not names:
         return None
@@ -388,35 +395,75 @@ def measure(cfg, steps, warmup, backward=True):
     return result
 
 
-def measure_reference_case(steps):
-    """The reference's own benchmark workload (AttentionBenchmarks.cpp:36-43,205-209): B2 x H12 x L1024 x d32, Q = 0.5,
-    K = V = 0.25, mask all ones, radius -1, no causal mask, through its flash entry point attention_fp32_forward_flash.
-    Its published figures are for an RX 6700 (README.md:63); they are quoted beside ours for context only."""
+# The reference's registered benchmark cases (ROCmKernels.Benchmark/src/AttentionBenchmarks.cpp:205-211), each through the
+# entry point it calls: (name, width, batch, heads, length, entry, backward).
+REFERENCE_CASES = (
+    ("Attention32 flash forward b2 h12 l1024", 32, 2, 12, 1024, "flash", False),
+    ("Attention32 forward b2 h12 l1024", 32, 2, 12, 1024, "simple", False),
+    ("Attention32 backward b2 h12 l1024", 32, 2, 12, 1024, "simple", True),
+    ("Attention32 tiled forward b2 h12 l1024", 32, 2, 12, 1024, "tiled", False),
+    ("Attention32 tiled backward b2 h12 l1024", 32, 2, 12, 1024, "tiled", True),
+    ("Attention64 forward b1 h4 l512", 64, 1, 4, 512, "simple", False),
+    ("Attention64 backward b1 h4 l512", 64, 1, 4, 512, "simple", True),
+)
+
+
+def measure_reference_cases(steps):
+    """The reference's own benchmark cases (AttentionBenchmarks.cpp:17-47,124-211): constant inputs Q = dO = 0.5,
+    K = V = 0.25, mask all ones, radius -1, no causal mask, each through the reference entry point it names (the
+    backward cases after one forward, as its State::Initialize does). FLOPs on its convention, 4*B*H*L^2*d forward and
+    8*... backward (every pair is visited). Constant inputs fix the results exactly: O = 0.25; every score of a row is
+    equal, so dP = dO.V = delta and dS = 0, giving dQ = dK = 0 and dV = sum_q P dO = 0.5, checked before timing.
+    Returns {case name: timing} and the flash case alone (the headline reference case)."""
     import torch
 
     from rocmkernels_amd import attention
 
     device = torch.device("cuda:0")
-    shape = (2, 12, 1024, 32)
-    q = torch.full(shape, 0.5, device=device)
-    k = torch.full(shape, 0.25, device=device)
-    v = torch.full(shape, 0.25, device=device)
-    mask = torch.ones((2, 1024), dtype=torch.uint8, device=device)
-    out = torch.empty(shape, device=device)
-    lse = torch.empty(shape[:3] + (2,), device=device)
+    out_cases = {}
+    for name, width, batch, heads, length, entry, with_backward in REFERENCE_CASES:
+        shape = (batch, heads, length, width)
+        q = torch.full(shape, 0.5, device=device)
+        k = torch.full(shape, 0.25, device=device)
+        v = torch.full(shape, 0.25, device=device)
+        du = torch.full(shape, 0.5, device=device)
+        mask = torch.ones((batch, length), dtype=torch.uint8, device=device)
+        out = torch.empty(shape, device=device)
+        lse = torch.empty(shape[:3] + (2,), device=device)
+        grads = (torch.empty(shape, device=device), torch.empty(shape, device=device), torch.empty(shape, device=device),
+                 torch.empty(shape[:3], device=device))
 
-    def launch():
-        attention.forward(q, k, v, mask, radius=-1, causal=False, output=out, lse=lse, entry="flash")
+        def forward():
+            attention.forward(q, k, v, mask, radius=-1, causal=False, output=out, lse=lse, entry=entry)
 
-    launch()
-    torch.cuda.synchronize()
-    if not bool((out == 0.25).all()):  # constant V: every output is exactly 0.25
-        raise RuntimeError("reference bench case: output is not 0.25")
-    flops = 4.0 * 24 * 1024 * 1024 * 32
-    timing = rates(time_samples(launch, [out, lse], steps), flops, flops)
-    timing["workload"] = "reference bench case: B2 x H12 x L1024 x d32, Q=0.5, K=V=0.25, no mask, not causal (flash entry)"
-    timing["reference_rx6700"] = {"ms_per_launch": 0.96, "tflops": 3.36, "source": "README.md:63 (RX 6700, gfx1031)"}
-    return {k: (round(v, 6) if isinstance(v, float) else v) for k, v in timing.items()}
+        def backward():
+            attention.backward(q, k, v, mask, out, lse, du, radius=-1, causal=False, entry=entry, grads=grads)
+
+        forward()
+        launch, results = forward, [out, lse]
+        if with_backward:
+            backward()
+            launch, results = backward, list(grads)
+        torch.cuda.synchronize()
+        if not bool((out == 0.25).all()):
+            raise RuntimeError(f"{name}: output is not 0.25")
+        if with_backward:
+            gq, gk, gv, _ = grads
+            worst = max(float(gq.abs().max()), float(gk.abs().max()), float((gv - 0.5).abs().max()))
+            if worst > 1e-5:
+                raise RuntimeError(f"{name}: gradients off their closed form by {worst:.3e}")
+        flops = (8.0 if with_backward else 4.0) * batch * heads * length * length * width
+        timing = rates(time_samples(launch, results, steps), flops, flops)
+        timing["entry"] = {"flash": "attention_fp32_forward_flash", "simple": "attention_fp32_forward",
+                           "tiled": "attention_fp32_forward_tiled"}[entry] if not with_backward else (
+            "attention_fp32_backward_tiled" if entry == "tiled" else "attention_fp32_backward")
+        if width == 64:
+            timing["entry"] = "attention64_fp32_backward" if with_backward else "attention64_fp32_forward"
+        out_cases[name] = rounded(timing)
+    flash = dict(out_cases[REFERENCE_CASES[0][0]])
+    flash["workload"] = "reference bench case: B2 x H12 x L1024 x d32, Q=0.5, K=V=0.25, no mask, not causal (flash entry)"
+    flash["reference_rx6700"] = {"ms_per_launch": 0.96, "tflops": 3.36, "source": "README.md:63 (RX 6700, gfx1031)"}
+    return out_cases, flash
 
 
 PEAK_FP16_MFMA_TFLOPS = 2500.0  # MI355X dense FP16 matrix peak (AMD public specification; no sparsity)
@@ -545,7 +592,7 @@ def main():
     result["rotary"] = measure_rotary(cfg, args.steps, args.warmup)
     result["generic_forward"] = measure_generic(cfg, args.steps)
     if args.config == 2:
-        result["reference_bench_case"] = measure_reference_case(args.steps)
+        result["reference_bench_cases"], result["reference_bench_case"] = measure_reference_cases(args.steps)
     result["cpu_baseline"] = cpu_baseline(args.config, args.cpu_seconds) if args.cpu_seconds > 0 else None
     print(json.dumps(result), flush=True)
 

@@ -235,3 +235,31 @@ def test_kernel_targets_link_common_publicly():
     with open(os.path.join(ROOT, "CMakeLists.txt")) as handle:
         cmake = handle.read()
     assert "target_link_libraries(${target_name} PUBLIC ROCmKernels.Common" in cmake
+
+
+def test_autograd_backward_mode_follows_torch_deterministic_mode_and_keeps_the_old_alias():
+    import warnings
+
+    import torch
+
+    from rocmkernels_amd import autograd
+
+    assert autograd.backward_mode(True) == (True, False)
+    assert autograd.backward_mode(False) == (False, False)
+    previous = torch.are_deterministic_algorithms_enabled()
+    try:
+        torch.use_deterministic_algorithms(True)
+        assert autograd.backward_mode() == (True, False)
+        torch.use_deterministic_algorithms(False)
+        assert autograd.backward_mode() == (False, False)
+    finally:
+        torch.use_deterministic_algorithms(previous)
+    with warnings.catch_warnings(record=True) as caught:
+        warnings.simplefilter("always")
+        assert autograd.backward_mode(fused_backward=True) == (False, True)
+        assert autograd.backward_mode(fused_backward=False) == (True, False)
+        assert autograd.backward_mode(False, fused_backward=True) == (False, True)
+    assert len(caught) == 3 and all(issubclass(w.category, DeprecationWarning) for w in caught)
+    with pytest.raises(ValueError), warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        autograd.backward_mode(True, fused_backward=True)

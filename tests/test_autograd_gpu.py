@@ -61,3 +61,37 @@ def test_autograd_lse_is_not_differentiable_and_second_call_reuses_nothing(devic
     q.grad = None
     autograd.attention_fp32(q, k, v, deterministic=True).sum().backward()
     assert torch.equal(first, q.grad)  # the deterministic backward is bit-reproducible
+
+
+def test_autograd_follows_torch_deterministic_mode(device):
+    # With torch's deterministic mode on, the default call runs the bit-reproducible backward: its gradients equal those
+    # of deterministic=True bit for bit (the fused default, whose dQ is summed with atomics, need not).
+    q, k, v = (torch.from_numpy(inputs.normal(s, (2, 3, 200, 32))).to(device).requires_grad_() for s in (41, 42, 43))
+    autograd.attention_fp32(q, k, v, causal=True, deterministic=True).sum().backward()
+    want = [t.grad.clone() for t in (q, k, v)]
+    previous = torch.are_deterministic_algorithms_enabled()
+    try:
+        torch.use_deterministic_algorithms(True)
+        for t in (q, k, v):
+            t.grad = None
+        autograd.attention_fp32(q, k, v, causal=True).sum().backward()
+    finally:
+        torch.use_deterministic_algorithms(previous)
+    for got, ref in zip((q.grad, k.grad, v.grad), want):
+        assert torch.equal(got, ref)
+
+
+def test_autograd_fused_backward_alias(device):
+    # The first version's keyword still works (with a DeprecationWarning): fused_backward=True runs the fused kernels,
+    # whose gradients meet the same tolerance as the deterministic ones.
+    shape = (1, 2, 96, 64)
+    q, k, v, du = (inputs.normal(seed, shape) for seed in (51, 52, 53, 54))
+    mask = np.ones((1, 96), np.uint8)
+    want = oracle.attention(q, k, v, mask, du, causal=True)
+    tq, tk, tv = (torch.from_numpy(a).to(device).requires_grad_() for a in (q, k, v))
+    with pytest.warns(DeprecationWarning):
+        out = autograd.attention_fp32(tq, tk, tv, causal=True, fused_backward=True)
+    (out * torch.from_numpy(du).to(device)).sum().backward()
+    for name, t in (("gq", tq), ("gk", tk), ("gv", tv)):
+        assert rel(t.grad.cpu().numpy(), want[name]) <= 1e-4, name
+

@@ -37,12 +37,26 @@ def test_visited_pairs_closed_forms():
 
 
 def test_forward_kernel_names_follow_the_launch_policy():
-    # 256 CUs: config 2 has 768 query tiles (3 per CU, persistent); configs 4 and 5 have 2048 and 4096 (dispatch
-    # order with 4 and 2 waves per tile).
+    # 256 CUs: config 2 has 768 query tiles (3 per CU, persistent); config 4 has 2048 causal items (costs vary: four
+    # waves per item); config 5 has 4096 items under a radius-256 window (uniform costs, 2048 resident slots at d = 64:
+    # one wave per item).
     assert bench.forward_kernel_name(bench.CONFIGS[2], 256) == "rk::attention_forward_kernel<32, false, true, 4, 3>"
     assert bench.forward_kernel_name(bench.CONFIGS[1], 256) == "rk::attention_forward_kernel<32, false, true, 4, 0>"
     assert bench.forward_kernel_name(bench.CONFIGS[4], 256) == "rk::attention_forward_kernel<64, false, true, 4, 0>"
-    assert bench.forward_kernel_name(bench.CONFIGS[5], 256) == "rk::attention_forward_kernel<64, false, true, 2, 0>"
+    assert bench.forward_kernel_name(bench.CONFIGS[5], 256) == "rk::attention_forward_kernel<64, false, true, 1, 0>"
+
+
+def test_roofline_kernels_have_profiled_traffic():
+    # The kernel each config's roofline names, and every kernel of each backward, has a counter row in
+    # profiles/traffic.json (rocprofv3 FETCH_SIZE / WRITE_SIZE of the same instance).
+    for config in (2, 3, 4, 5):
+        name = bench.forward_kernel_name(bench.CONFIGS[config], 256)
+        assert bench.load_traffic(name, config) is not None, (config, name)
+        for part in ("backward", "backward_deterministic"):
+            rows = bench.backward_traffic(config, part)
+            assert rows is not None and len(rows["kernels"]) == 2, (config, part)
+            fused = any("fused_backward" in n or "band" in n for n in rows["kernels"])
+            assert fused == (part == "backward"), (config, part, rows["kernels"])
 
 
 def test_cpu_baseline_reports_single_thread_and_all_core_rates():
