@@ -352,7 +352,7 @@ def rates(timing, flops_convention, flops_visited, eager=None):
     return out
 
 
-def measure(cfg, steps, warmup, backward=True):
+def measure(cfg, steps, warmup, backward=True, forward_timed=True):
     import torch
 
     from rocmkernels_amd import attention
@@ -379,8 +379,9 @@ def measure(cfg, steps, warmup, backward=True):
     stream = torch.cuda.current_stream()
     result = {"visited_pairs": pairs}
     width = cfg["width"]
-    eager = time_eager(forward, steps, warmup, stream)
-    result["forward"] = rates(time_samples(forward, [out, lse], steps), 4.0 * full * width, 4.0 * pairs * width, eager)
+    if forward_timed:
+        eager = time_eager(forward, steps, warmup, stream)
+        result["forward"] = rates(time_samples(forward, [out, lse], steps), 4.0 * full * width, 4.0 * pairs * width, eager)
     if backward:
         # The default backward may accumulate dQ with atomics (checked against the eager result within 1e-5); the
         # deterministic one is checked bit for bit.
@@ -511,6 +512,20 @@ def measure_generic(cfg, steps):
     return out
 
 
+def measure_part(part, cfg, args):
+    """One part of the line alone, for profiler runs (rocprofv3 then sees only its kernels): the forward and the
+    backward of the config (the backward after one forward, both backward implementations), the generic forward, the
+    reference cases or rotary."""
+    if part in ("forward", "backward"):
+        measured = measure(cfg, args.steps, args.warmup, backward=part == "backward", forward_timed=part == "forward")
+        return {k: rounded(v) if isinstance(v, dict) else v for k, v in measured.items()}
+    if part == "generic":
+        return measure_generic(cfg, args.steps)
+    if part == "reference":
+        return measure_reference_cases(args.steps)[0]
+    return measure_rotary(cfg, args.steps, args.warmup)
+
+
 def rounded(d):
     return {k: (round(v, 6) if isinstance(v, float) else v) for k, v in d.items()}
 
@@ -530,6 +545,8 @@ def main():
     parser.add_argument("--samples", type=int, default=SAMPLES_MIN,
                         help="timed samples per measurement (default 20, the harness's minimum; fewer only for profiler runs)")
     parser.add_argument("--sample-ms", type=float, default=SAMPLE_MS, help="minimum length of one sample in ms")
+    parser.add_argument("--only", choices=("forward", "backward", "generic", "reference", "rotary"), default=None,
+                        help="time one part alone and print its figures (for profiler runs; not the driver's line)")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
                         help="first copy a buffer of this many MiB on the device (reference for rocprofv3 byte counters)")
     args = parser.parse_args()
@@ -552,6 +569,9 @@ def main():
     SAMPLES_MIN = max(1, args.samples)
     SAMPLE_MS = args.sample_ms
     cfg = CONFIGS[args.config]
+    if args.only is not None:
+        print(json.dumps({"only": args.only, "config": cfg["workload"], "result": measure_part(args.only, cfg, args)}), flush=True)
+        return
     measured = measure(cfg, args.steps, args.warmup, backward=not args.no_backward)
     fwd = measured["forward"]
     kernel = forward_kernel_name(cfg, torch.cuda.get_device_properties(0).multi_processor_count)

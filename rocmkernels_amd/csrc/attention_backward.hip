@@ -811,15 +811,30 @@ void launch_dkdv_mapped(const BackwardArgs &a, const int cus, hipStream_t stream
 }
 
 
+// Smallest number of 128-key blocks per CU (num / den) at which Auto takes the band kernel under a radius window.
+struct BlocksPerCu {
+    int num, den;
+};
+constexpr BlocksPerCu kBandMinBlocksPerCu{5, 8};
+
 template<int D, bool VEC>
 hipError_t run(BackwardStage stage, const BackwardArgs &a, const int cus, hipStream_t stream) {
     const int64_t kitems = static_cast<int64_t>((a.keys + kTile - 1) / kTile) * a.batch * a.heads;
+    const int64_t kblocks = static_cast<int64_t>((a.keys + kBlockKeys - 1) / kBlockKeys) * a.batch * a.heads;
     // The fused key-block kernels need 128-bit access; without it the deterministic kernels measured faster.
     // Auto takes the fused kernels wherever they exist (128-bit access): under a radius window the band kernel against
     // the deterministic pair, causal, measured 146.4 against 160.3 us at D = 32 (16 sequences x 8192 tokens, radius
     // 256), 124.9 against 147.8 us (32 x 2048, radius 512), 101.9 against 103.4 us (32 x 4096, radius 128), and 258
-    // against 287 us at D = 64 (config 5).
-    if (stage == kBackwardAuto) stage = VEC ? kBackwardFused : kBackwardAll;
+    // against 287 us at D = 64 (config 5). The band kernel runs one persistent workgroup per 128-key block and never
+    // splits a block, so with fewer blocks than a grid that fills the CUs it leaves them idle while the deterministic
+    // pair spreads 32-row tiles over every CU: measured, causal, 1 x 8192 at D = 64, radius 256 (64 blocks) 64.9
+    // against 40.0 us, 2 x 8192 (128 blocks) 67.5 against 59.0 us, 4 x 8192 (256 blocks) 74.0 against 105.8 us; at
+    // D = 32, 64 / 128 / 256 blocks 38.0 / 39.1 / 42.4 against 22.2 / 32.0 / 58.3 us. So under a radius window Auto
+    // takes the band kernel only from kBandMinBlocksPerCu blocks per CU.
+    if (stage == kBackwardAuto) {
+        const bool band_fills = a.radius < 0 || kblocks * kBandMinBlocksPerCu.den >= static_cast<int64_t>(cus) * kBandMinBlocksPerCu.num;
+        stage = VEC && band_fills ? kBackwardFused : kBackwardAll;
+    }
     if (stage == kBackwardFused) {
         // Key-block kernels (one dQ add per element per 128 keys): without a radius window the piece-planned one; under a
         // radius window the band kernel, whose skewed walk visits each key tile's own band only (the key-block walk over

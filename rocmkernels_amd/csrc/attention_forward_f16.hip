@@ -15,6 +15,9 @@
 //     ds_read_b64_tr_b16 (a transposing 16-bit LDS read, two per MFMA); otherwise each element is a 16-bit load.
 //   * The online softmax (lazy re-basing, exp2 with the scale folded into one FMA), the masks, the work mapping and
 //     the merge of the waves sharing a query tile follow attention_forward.hip.
+//   * Two kernels: attention_forward_f16_kernel gives each wave its own K/V tiles (1, 2 or 4 waves per query tile);
+//     at d = 64 on grids that fill the chip, attention_forward_f16_shared_kernel has the waves of a workgroup (four query
+//     tiles of one sequence) share each K/V tile through LDS, a quarter of the per-wave kernel's L2 traffic.
 #include "attention_device.hpp"
 #include "attention_launch.hpp"
 
@@ -367,6 +370,270 @@ __global__ __launch_bounds__(kThreads) void attention_forward_f16_kernel(const T
     }
 }
 
+// Shared K/V tiles: QB query tiles of one sequence per workgroup (d = 64, 16-byte aligned rows, every stride a
+// multiple of 8). Wave w of the workgroup owns query tile QB·block + w mod QB and key stream w / QB: the KS streams
+// take alternate key tiles of the union of the workgroup's windows. The QB waves of a stream stream its tiles together:
+// each loads 1/QB of a tile's K and V rows (whole 128-byte lines) into the stream's double-buffered LDS stage, which all
+// of them read, so every K/V byte crosses from L2 once per QB waves instead of once per wave, and the loads run two
+// tiles ahead of their use. Per step: one workgroup barrier; then the next tile's rows go from registers into the
+// other stage (V rows of masked keys as zeros) and the loads of the tile after it are issued; then each wave whose
+// window meets the tile computes it as attention_forward_f16_kernel does (K's row layout read from the stage with
+// 128-bit LDS reads, V's operand with transposing reads). Every wave runs every step (the barriers are uniform); a wave
+// past the last query tile or outside the tile's window only loads and stores its share. With KS = 2 the second
+// stream's softmax state is merged into the first through LDS at the end (a fixed order: deterministic). The kernel
+// is held to 128 VGPRs, so four waves fit on every SIMD.
+template<int D, int QB, int KS>
+__global__ __launch_bounds__(kWave * QB * KS) __attribute__((amdgpu_waves_per_eu(4))) void attention_forward_f16_shared_kernel(
+        const TensorH q, const TensorH k, const TensorH v, const uint8_t *__restrict__ mask, _Float16 *__restrict__ out,
+        const int osb, const int osh, const int ost, float *__restrict__ lse, const Shape s, const float scale) {
+    static_assert(D == 64, "shared K/V tiles are for 64-wide heads (at d = 32 the per-wave kernel is faster)");
+    static_assert((QB == 2 || QB == 4) && (KS == 1 || KS == 2));
+    constexpr int KC = D / 16;                  // MFMAs per Sᵀ tile
+    constexpr int DT = D / 32;                  // 32-feature output slices
+    constexpr int KSTR = D + 8;                 // K stage row stride (halves): 16 bytes of padding, conflict-free row reads
+    constexpr int CPR = D / 8;                  // 16-byte chunks per row
+    constexpr int WCH = kTile * CPR / QB;       // chunks of a tile (K or V) loaded by one wave
+    constexpr int NLOAD = (WCH + kWave - 1) / kWave;
+    constexpr int ACTIVE = WCH < kWave ? WCH : kWave; // lanes that load
+    constexpr int KHALVES = kTile * KSTR, VHALVES = kTile * kVStride<D>;
+    constexpr int STAGE_BYTES = 2 * KS * (KHALVES + VHALVES) * 2;
+    constexpr int NREG = 16 * DT + 3;           // merged per lane: m, l, mc and the output accumulators
+    constexpr int MERGE_BYTES = KS > 1 ? QB * NREG * kWave * 4 : 0;
+    __shared__ __align__(16) unsigned char smem[STAGE_BYTES > MERGE_BYTES ? STAGE_BYTES : MERGE_BYTES];
+    // Stage (stream x, parity p): K rows then V rows.
+    auto kstage = [&](const int x, const int p) { return reinterpret_cast<_Float16 *>(smem) + (2 * x + p) * (KHALVES + VHALVES); };
+    auto vstage = [&](const int x, const int p) { return kstage(x, p) + KHALVES; };
+
+    const int lane = threadIdx.x & (kWave - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int qi = wave % QB;     // query tile of the workgroup
+    const int stream = wave / QB; // key stream
+    const int col = lane & 31;
+    const int h = lane >> 5;
+    const float c2 = scale * kLog2e;
+
+    // Workgroup g takes query block g / seqs of sequence g % seqs: with B·H a multiple of 8 (workgroup g runs on XCD
+    // g mod 8), each XCD streams the K/V rows of its own eighth of the sequences from its L2.
+    const int seqs = s.batch * s.heads;
+    const int seq = static_cast<int>(blockIdx.x) % seqs;
+    const int qb = static_cast<int>(blockIdx.x) / seqs;
+    const int b = seq / s.heads, head = seq - b * s.heads;
+    const int q0 = (qb * QB + qi) * kTile;
+    const int query = q0 + col;
+    const bool tile_valid = q0 < s.queries;
+
+    // Keys [first, last) seen by query tile t0's queries.
+    auto key_window = [&](const int t0, int &first, int &last) __attribute__((always_inline)) {
+        first = 0;
+        last = s.keys;
+        if (s.radius >= 0) {
+            first = max(0, t0 - s.radius);
+            last = min(last, t0 + kTile + s.radius);
+        }
+    };
+    // This wave's window, and the workgroup's union (from its first query tile's start to its last valid one's end).
+    int first, last, ufirst, ulast, unused;
+    key_window(q0, first, last);
+    key_window(qb * QB * kTile, ufirst, unused);
+    key_window(min(qb * QB + QB - 1, (s.queries - 1) / kTile) * kTile, unused, ulast);
+    const int ntiles = ulast > ufirst ? (ulast - ufirst + kTile - 1) / kTile : 0;
+    const int nsteps = (ntiles + KS - 1) / KS; // steps of every stream; tile of stream x at step i: i·KS + x
+    const int wlo = window_lo(s, query);
+    const int whi = window_hi(s, query);
+
+    auto seq_base = [&](const TensorH &t) {
+        return t.data + (static_cast<int64_t>(b) * t.sb + static_cast<int64_t>(head) * t.sh);
+    };
+    const Buffer qbuf = make_buffer(seq_base(q), sequence_bytes_h(s.queries, q.st, D));
+    const Buffer kbuf = make_buffer(seq_base(k), sequence_bytes_h(s.keys, k.st, D));
+    const Buffer vbuf = make_buffer(seq_base(v), sequence_bytes_h(s.keys, v.st, D));
+    const Buffer mbuf = make_buffer(mask + static_cast<int64_t>(b) * s.keys, static_cast<uint32_t>(s.keys));
+    const uint32_t kstep = 2u * k.st;
+    const uint32_t vstep = 2u * v.st;
+
+    f16x8 qr[KC];
+#pragma unroll
+    for (int i = 0; i < KC; ++i)
+        qr[i] = load8h<true>(qbuf, tile_valid ? static_cast<uint32_t>(query) * (2u * q.st) + 2u * (16 * i + 8 * h) : kNoRow);
+
+    // This lane's chunks of its stream's tiles: chunk c = qi * WCH + 64 i + lane, row c / CPR, 16-byte column c mod CPR.
+    const bool loader = lane < ACTIVE;
+    struct Set {
+        u32x4 k[NLOAD], v[NLOAD];
+        int mbyte;
+    };
+    auto chunk_row = [&](const int i) { return (qi * WCH + kWave * i + lane) / CPR; };
+    auto chunk_col = [&](const int i) { return (qi * WCH + kWave * i + lane) % CPR; };
+    // The loads of this stream's step i. Every step issues them unconditionally (a tile past the last one reads 0
+    // through the range check, offset kNoRow), so the loop has no branch around them.
+    auto issue = [&](Set &st, const int i) __attribute__((always_inline)) {
+        const int t = i * KS + stream;
+        const bool live = t < ntiles;
+        const int key0 = ufirst + t * kTile;
+        st.mbyte = buffer_load_byte(mbuf, live ? static_cast<uint32_t>(key0 + col) : kNoRow); // keys past the end read 0
+#pragma unroll
+        for (int j = 0; j < NLOAD; ++j) {
+            const uint32_t row = static_cast<uint32_t>(key0 + chunk_row(j));
+            const uint32_t c16 = 16u * static_cast<uint32_t>(chunk_col(j));
+            const bool on = live && loader;
+            st.k[j] = __builtin_amdgcn_raw_buffer_load_b128(kbuf, static_cast<int>(on ? row * kstep + c16 : kNoRow), 0, 0);
+            st.v[j] = __builtin_amdgcn_raw_buffer_load_b128(vbuf, static_cast<int>(on ? row * vstep + c16 : kNoRow), 0, 0);
+        }
+    };
+    // Writes a loaded tile into this stream's stage p; returns the tile's key-mask ballot.
+    auto commit = [&](const Set &st, const int p) __attribute__((always_inline)) {
+        const uint32_t bits = static_cast<uint32_t>(__ballot(st.mbyte != 0));
+        if (loader) {
+            _Float16 *const ks = kstage(stream, p);
+            _Float16 *const vs = vstage(stream, p);
+#pragma unroll
+            for (int j = 0; j < NLOAD; ++j) {
+                const int r = chunk_row(j), c = chunk_col(j);
+                const bool kept = (bits >> r) & 1u;
+                *reinterpret_cast<u32x4 *>(ks + r * KSTR + 8 * c) = st.k[j];
+                *reinterpret_cast<u32x4 *>(vs + r * kVStride<D> + 8 * c) = kept ? st.v[j] : u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+        return bits;
+    };
+
+    constexpr float kLazy = 8.0f; // p = exp2(s·c2 - mc) <= 2^8: also within fp16 range
+    const float lazy_raw = kLazy / c2;
+    float m_half = -INFINITY, m_lazy = -INFINITY, mc = -INFINITY, mcx = 0.0f, l_run = 0.0f;
+    f32x16 o[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t) o[t] = f32x16{};
+    const int vread = (4 * h + ((lane & 15) >> 2)) * kVStride<D> + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+
+    // The product of the tile at key0 from this stream's stage p for this wave's query tile.
+    auto compute = [&](const int p, const int key0, const uint32_t bits) __attribute__((always_inline)) {
+        if (!tile_valid || bits == 0 || key0 >= last || key0 + kTile <= first) return;
+        const _Float16 *kp = kstage(stream, p) + col * KSTR + 8 * h;
+        const _Float16 *vs = vstage(stream, p);
+        f32x16 sc{};
+#pragma unroll
+        for (int i = 0; i < KC; ++i) sc = mfma16(*reinterpret_cast<const f16x8 *>(kp + 16 * i), qr[i], sc);
+        // V's operands are read once the K operands are consumed (their registers are free again); the softmax below
+        // covers the reads' LDS latency.
+        __builtin_amdgcn_sched_barrier(0);
+        f16x8 vop[DT][2];
+        vop[0][0] = read_v_operand<D, 0, 0>(vs, vread);
+        vop[0][1] = read_v_operand<D, 0, 1>(vs, vread);
+        if constexpr (DT > 1) {
+            vop[DT - 1][0] = read_v_operand<D, DT - 1, 0>(vs, vread);
+            vop[DT - 1][1] = read_v_operand<D, DT - 1, 1>(vs, vread);
+        }
+        if (bits != 0xffffffffu || !tile_in_window(s, q0, key0)) {
+            const uint32_t visible = (bits & bit_range(wlo - key0, whi - key0)) >> (4 * h);
+#pragma unroll
+            for (int j = 0; j < 16; ++j) sc[j] = (visible >> (8 * (j >> 2) + (j & 3))) & 1u ? sc[j] : -INFINITY;
+        }
+        float mx = m_half;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) mx = fmaxf(mx, sc[j]);
+        m_half = mx;
+        if (__builtin_expect(__ballot(m_half > m_lazy) != 0, 0)) {
+            const float m_row = halves_max(m_half);
+            const float mc_new = m_row == -INFINITY ? -INFINITY : m_row * c2;
+            m_lazy = m_row + lazy_raw;
+            const float alpha = mc_new == -INFINITY ? 1.0f : exp2_fast(mc - mc_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int t2 = 0; t2 < DT; ++t2) o[t2] *= alpha;
+            mc = mc_new;
+            mcx = mc_new == -INFINITY ? 0.0f : mc_new;
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) sc[j] = exp2_fast(fmaf(sc[j], c2, -mcx));
+        float psum = sc[0];
+#pragma unroll
+        for (int j = 1; j < 16; ++j) psum += sc[j];
+        l_run += psum;
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            f16x8 pv;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) pv[j] = static_cast<_Float16>(sc[8 * u + j]);
+#pragma unroll
+            for (int t2 = 0; t2 < DT; ++t2) o[t2] = mfma16(vop[t2][u], pv, o[t2]);
+        }
+    };
+
+    // Step i of stream x: tile i·KS + x, loaded into the register set two steps before, written to stage i mod 2 one
+    // step before. A step: barrier (stage i mod 2 is complete; every wave is done reading the other stage), step i + 1's
+    // tile from the registers into the other stage and step i + 2's loads into the registers, then step i's product:
+    // the loads have a whole step (the product and the barrier) to land.
+    if (nsteps > 0) {
+        Set st;
+        issue(st, 0);
+        uint32_t bits = commit(st, 0);
+        issue(st, 1);
+        for (int i = 0; i < nsteps; ++i) {
+            __syncthreads();
+            const uint32_t next_bits = commit(st, (i + 1) & 1);
+            issue(st, i + 2);
+            const int t = i * KS + stream;
+            if (t < ntiles) compute(i & 1, ufirst + t * kTile, bits);
+            bits = next_bits;
+        }
+    }
+
+    const float m_run = halves_max(m_half);
+    float m_all = m_run, base = mc == -INFINITY ? 0.0f : mc, l_all = l_run;
+    if constexpr (KS > 1) {
+        // Stream 1 hands (row maximum, sum, base, accumulators) to stream 0 through LDS; stream 0 rescales both to the
+        // larger base and adds.
+        float *const slot = reinterpret_cast<float *>(smem) + qi * (NREG * kWave) + lane;
+        __syncthreads(); // every wave is done with the stages
+        if (stream == 1) {
+            slot[0] = m_run;
+            slot[kWave] = l_run;
+            slot[2 * kWave] = mc;
+#pragma unroll
+            for (int t = 0; t < DT; ++t) {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) slot[(3 + 16 * t + j) * kWave] = o[t][j];
+            }
+        }
+        __syncthreads();
+        if (stream == 1) return;
+        const float m1 = slot[0], l1 = slot[kWave], mc1 = slot[2 * kWave];
+        m_all = fmaxf(m_run, m1);
+        const float mc_all = fmaxf(mc, mc1);
+        base = mc_all == -INFINITY ? 0.0f : mc_all;
+        const float a0 = exp2_fast(mc - base), a1 = exp2_fast(mc1 - base);
+        l_all = fmaf(l1, a1, l_run * a0);
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) o[t][j] = fmaf(slot[(3 + 16 * t + j) * kWave], a1, o[t][j] * a0);
+        }
+    }
+
+    if (!tile_valid || query >= s.queries) return;
+    l_all = halves_sum(l_all);
+    const float sum_at_max = m_all == -INFINITY ? l_all : l_all * exp2_fast(base - m_all * c2);
+    const bool nan_row = isnan(l_all);
+    const bool has_keys = l_all > 0.0f;
+    const float factor = has_keys ? 1.0f / l_all : (nan_row ? NAN : 0.0f);
+    _Float16 *orow = out + static_cast<int64_t>(b) * osb + static_cast<int64_t>(head) * osh + static_cast<int64_t>(query) * ost;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            f16x4 x;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[i] = static_cast<_Float16>(has_keys ? o[t][4 * u + i] * factor : factor);
+            *reinterpret_cast<f16x4 *>(orow + 32 * t + 8 * u + 4 * h) = x;
+        }
+    }
+    if (h == 0) {
+        const int64_t row = static_cast<int64_t>(seq) * s.queries + query;
+        lse[2 * row] = has_keys ? m_all * scale : (nan_row ? NAN : -INFINITY);
+        lse[2 * row + 1] = has_keys ? sum_at_max : (nan_row ? NAN : 0.0f);
+    }
+}
+
 namespace {
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -382,6 +649,16 @@ bool fits_h(const int rows, const rocmkernels_strides &s, const int width) {
 
 TensorH tensor_h(const void *p, const rocmkernels_strides &s) {
     return TensorH{static_cast<const _Float16 *>(p), s.batch, s.head, s.token};
+}
+
+template<int D, int QB, int KS>
+void launch_shared(const HalfForwardArgs &a, const int64_t groups, hipStream_t stream) {
+    const Shape shape{a.batch, a.heads, a.queries, a.keys, a.radius, 0};
+    const float scale = 1.0f / sqrtf(static_cast<float>(D));
+    hipLaunchKernelGGL((attention_forward_f16_shared_kernel<D, QB, KS>), dim3(static_cast<unsigned>(groups)), dim3(kWave * QB * KS), 0,
+            stream,
+            tensor_h(a.q, a.qs), tensor_h(a.k, a.ks), tensor_h(a.v, a.vs), reinterpret_cast<const uint8_t *>(a.mask),
+            static_cast<_Float16 *>(a.output), a.os.batch, a.os.head, a.os.token, a.lse, shape, scale);
 }
 
 template<int D, bool VEC, int SPLIT, bool STAGE_V>
@@ -422,7 +699,25 @@ void dispatch(const HalfForwardArgs &a, const int64_t items, const int cus, hipS
     bool stage = false;
     if constexpr (D >= 32) stage = vec && aligned16(a.v) && strides8(a.vs);
     if (stage) {
-        if constexpr (D >= 32) launch_split<D, true, true>(a, items, split, stream);
+        if constexpr (D >= 32) {
+            // d = 64: shared K/V tiles (four query tiles per workgroup) when those workgroups give every CU one; two key
+            // streams per workgroup (eight waves) until there are four workgroups per CU, so that each SIMD holds four
+            // waves. Measured on the generic fp16 forward (the per-wave kernel against the shared one): 32 x 2048
+            // 76.7 -> 48.3 µs (two streams; one: 51.8), 16 x 8192 radius 256 51.9 -> 34.7 µs (one stream), 8 x 16 x
+            // 1024 80.9 -> 49.9 µs. At d = 32 the per-wave kernel stays: its tiles carry half the bytes, and the
+            // shared kernel's barrier per tile cost more than the loads it saves (24 x 1024 9.6 against 13.5 µs,
+            // 2 x 16 x 2048 radius 300 14.3 against 17.1 µs, 4 x 8 x 2048 37.1 against 36.0 µs).
+            if constexpr (D == 64) {
+                const int64_t seqs = static_cast<int64_t>(a.batch) * a.heads;
+                const int64_t groups = seqs * ((a.queries + 4 * kTile - 1) / (4 * kTile));
+                if (groups >= cus) {
+                    if (groups >= 4 * cus) launch_shared<64, 4, 1>(a, groups, stream);
+                    else launch_shared<64, 4, 2>(a, groups, stream);
+                    return;
+                }
+            }
+            launch_split<D, true, true>(a, items, split, stream);
+        }
     } else if (vec) {
         launch_split<D, true, false>(a, items, split, stream);
     } else {

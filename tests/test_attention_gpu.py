@@ -26,14 +26,15 @@ BACKWARD_MODES = ("default", "deterministic")
 
 def run_both(device, q, k, v, du, mask, radius=-1, causal=False, fwd="flash", bwd="simple", fcode=None, bcode=None, mode=None):
     """Forward, then backward on the forward's O and lse. ``mode`` None: the entry named by ``bwd`` (the *_ex default
-    when causal); "default": the *_ex backward without a mode flag (fused where it exists); "deterministic": the *_ex
-    backward with ROCMKERNELS_ATTENTION_DETERMINISTIC."""
+    when causal); "default": the *_ex backward without a mode flag (the faster one for the call); "fused": the *_ex
+    backward with ROCMKERNELS_ATTENTION_FUSED_BACKWARD (the band kernel under a radius window); "deterministic": the
+    *_ex backward with ROCMKERNELS_ATTENTION_DETERMINISTIC."""
     tq, tk, tv, tdu, tm = to_dev(device, q, k, v, du, mask)
     out, lse = attention.forward(tq, tk, tv, tm, radius=radius, causal=causal, entry=fwd, code=fcode)
     if mode is not None:
         bwd = "ex"
     gq, gk, gv, delta = attention.backward(tq, tk, tv, tm, out, lse, tdu, radius=radius, causal=causal, entry=bwd, code=bcode,
-                                           deterministic=mode == "deterministic")
+                                           deterministic=mode == "deterministic", fused=mode == "fused")
     return host(out, lse, gq, gk, gv, delta)
 
 
@@ -524,3 +525,30 @@ def test_large_logits(device, width, batch, heads, length, gain, radius, causal,
     # Per row the bound is 1e-2 here: a row dominated by one key has P close to one-hot, so dS = P(dP - delta) nearly
     # cancels and its dQ is small against the terms it is summed from (the normwise bound is the usual 1e-4).
     check_backward(gq, gk, gv, delta, want, label, row_tol=1e-2)
+
+
+@pytest.mark.parametrize("width", [32, 64])
+@pytest.mark.parametrize("mode", ["fused", "deterministic"])
+@pytest.mark.parametrize("radius,causal", [(0, False), (-1, True)])
+def test_single_key_rows_dq_is_fp32_rounding_of_zero(device, width, mode, radius, causal):
+    # A query with one visible key (every query under radius 0; query 0 under the causal mask) has P = 1 and O = v, so
+    # dS = P (dP - delta) subtracts two FP32 dot products of the same vectors: dP = dO.v summed by the MFMA chain and
+    # delta = dO.O summed by the delta tree. The exact dQ (and, under radius 0, dK) is 0, and the oracle gives exactly
+    # 0; the kernels give the rounding residual of that cancellation. These rows hold the suite's largest per-row dQ
+    # errors (an all-zero row is judged against the per-row floor, 1e-3 of the tensor's largest value). Bound them by
+    # the FP32 rounding of the cancelling sums: |dQ| <= 4 * D * 2^-24 * sum_c |dO_c v_c| * max_f |k_f| / sqrt(D).
+    batch, heads, length = 2, 3, 200
+    q, k, v, du = normal_case(1200 + width, width, batch, heads, length, length)
+    mask = np.ones((batch, length), np.uint8)
+    out, lse, gq, gk, gv, delta = run_both(device, q, k, v, du, mask, radius=radius, causal=causal, mode=mode)
+    rows = np.arange(length) if radius == 0 else np.array([0])
+    gamma = 4.0 * width * 2.0 ** -24 / np.sqrt(width)
+    dots = np.abs(du[:, :, rows].astype(np.float64) * v[:, :, rows]).sum(-1)  # the single key of row r is key r
+    bound_q = gamma * dots * np.abs(k[:, :, rows]).max(-1)
+    got_q = np.abs(gq[:, :, rows]).max(-1)
+    assert np.all(got_q <= bound_q), f"dQ {got_q.max():.3e} above its rounding bound (ratio {(got_q / bound_q).max():.2f})"
+    if radius == 0:  # key r is seen by query r alone: dK of every key is the same residual times q
+        bound_k = gamma * dots * np.abs(q[:, :, rows]).max(-1)
+        got_k = np.abs(gk[:, :, rows]).max(-1)
+        assert np.all(got_k <= bound_k), f"dK {got_k.max():.3e} above its rounding bound (ratio {(got_k / bound_k).max():.2f})"
+        assert np.abs(gv - du).max() <= 1e-5

@@ -234,3 +234,54 @@ def test_generic_fp16_two_waves_per_item(device, batch, heads, length, width, ra
     want = oracle.attention(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32), mask, radius=radius)
     out, lse = run(device, q, k, v, mask, radius=radius)
     check(out, lse, want, "f16", f"{batch}x{heads}x{length} d{width} r{radius}")
+
+
+SHARED_CASES = [
+    (64, 4, 100, 77, -1, True),     # 256 sequences x 4 query tiles (the last partial): four tiles per workgroup
+    (32, 8, 130, 300, 21, True),    # 5 query tiles (a half-empty second workgroup), radius window, more keys than queries
+    (130, 1, 128, 128, -1, False),  # 130 workgroups, fewer than the CUs: the per-wave kernel at both widths
+    (65, 4, 33, 20, 5, True),       # 2 query tiles, fewer keys than one tile, the window wider than the keys
+    (16, 16, 256, 256, 64, False),  # radius window: each workgroup streams the union of its four tiles' windows
+    (64, 16, 128, 64, 7, True),     # 1024 workgroups (four per CU): one key stream
+]
+
+
+@pytest.mark.parametrize("width", [32, 64])
+@pytest.mark.parametrize("batch,heads,queries,keys,radius,pad", SHARED_CASES)
+def test_generic_fp16_shared_kv_tiles(device, width, batch, heads, queries, keys, radius, pad):
+    # At d = 64, grids of at least one workgroup of four query tiles per CU take the shared K/V kernel (the waves of a
+    # workgroup stream its K/V tiles through LDS once for all of them; two key streams per workgroup below four
+    # workgroups per CU); the shapes cover partial workgroups, Lq != Lk, radius windows and key padding, with one and two
+    # streams. At d = 32 the same shapes run the per-wave kernel.
+    seed = 1000 + width + queries + keys
+    q = inputs.normal(seed, (batch, heads, queries, width)).astype(np.float16)
+    k = inputs.normal(seed + 1, (batch, heads, keys, width)).astype(np.float16)
+    v = inputs.normal(seed + 2, (batch, heads, keys, width)).astype(np.float16)
+    mask = np.ones((batch, keys), np.uint8)
+    if pad:
+        lengths = inputs.uniform_int(seed + 3, batch, 1, keys)
+        mask = (np.arange(keys)[None, :] < lengths[:, None]).astype(np.uint8)
+        mask[0, 0] = 0
+    want = oracle.attention(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32), mask, radius=radius)
+    out, lse = run(device, q, k, v, mask, radius=radius)
+    check(out, lse, want, "f16", f"{batch}x{heads} {queries}x{keys} d{width} r{radius} shared")
+
+
+@pytest.mark.parametrize("width", [32, 64])
+def test_generic_fp16_shared_kv_tiles_garbage_and_masked_batch(device, width):
+    # Masked keys holding inf (K) and NaN (V) contribute nothing through the shared stages (their V rows are written
+    # as zeros, their scores dropped), and a fully masked batch gives O = 0, lse = {-inf, 0}.
+    batch, heads, queries, keys = 32, 8, 96, 100
+    q, k, v = (inputs.normal(1100 + i, (batch, heads, n, width)).astype(np.float16) for i, n in enumerate((queries, keys, keys)))
+    mask = np.ones((batch, keys), np.uint8)
+    mask[0, 40:48] = 0
+    mask[0, 90:] = 0
+    mask[1, 5] = 0
+    mask[2] = 0
+    want = oracle.attention(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32), mask)
+    hidden = mask[:, None, :, None] == 0
+    k = np.where(hidden, np.float16(np.inf), k)
+    v = np.where(hidden, np.float16(np.nan), v)
+    out, lse = run(device, q, k, v, mask)
+    check(out, lse, want, "f16", f"d{width} shared, garbage in masked rows")
+    assert np.all(out[2] == 0.0) and np.all(lse[2, ..., 0] == -np.inf) and np.all(lse[2, ..., 1] == 0.0)
