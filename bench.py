@@ -468,6 +468,32 @@ def measure_reference_cases(steps):
 
 
 PEAK_FP16_MFMA_TFLOPS = 2500.0  # MI355X dense FP16 matrix peak (AMD public specification; no sparsity)
+# Softmax work of one 32 x 32 score tile on one wave, the fewest instructions the online softmax needs per tile:
+# 8 three-input maxima and 1 compare (row maximum, re-base test), 16 FMAs (scale and offset), 16 exponentials,
+# 16 adds (row sum), 8 packed conversions to fp16; measured issue costs on gfx950: 4 cycles per VALU instruction,
+# 8 per v_exp_f32. FP16 MFMAs co-issue with VALU work, so this is the fp16 forward's ALU bound.
+F16_TILE_VALU = 49
+F16_TILE_TRANS = 16
+F16_TILE_CYCLES = 4 * F16_TILE_VALU + 8 * F16_TILE_TRANS
+SIMDS = 1024          # 256 CUs x 4 SIMDs
+CLOCK_GHZ = 2.4       # the clock of the published peaks
+
+
+def computed_tiles(queries, keys, radius, seqs):
+    """32 x 32 score tiles the forward kernels compute: for each 32-query tile, the whole key tiles from the first key
+    any of its queries sees to the last (no causal flag: the generic entry point has none)."""
+    total = 0
+    for q0 in range(0, queries, 32):
+        first, last = 0, keys
+        if radius >= 0:
+            first, last = max(0, q0 - radius), min(keys, q0 + 32 + radius)
+        total += -(-(last - first) // 32) if last > first else 0
+    return total * seqs
+
+
+def f16_valu_ceiling_us(tiles):
+    """ALU bound of the fp16 forward: every SIMD issuing the softmax work of its share of the tiles, nothing else."""
+    return tiles / SIMDS * F16_TILE_CYCLES / (CLOCK_GHZ * 1e3)
 
 
 def measure_generic(cfg, steps):
@@ -507,6 +533,14 @@ def measure_generic(cfg, steps):
                      "ms_p95": round(timing["ms_p95"], 6), "tflops_visited": round(tflops, 4), "peak_tflops": peak,
                      "frac_of_mfma_peak": round(tflops / peak, 4), "samples": timing["samples"],
                      "launches_per_sample": timing["launches_per_sample"]}
+        if name == "f16":
+            tiles = computed_tiles(length, length, radius, batch * heads)
+            ceiling = f16_valu_ceiling_us(tiles)
+            out[name]["valu_ceiling"] = {
+                "us": round(ceiling, 4), "frac": round(ceiling / (timing["ms_per_launch"] * 1e3), 4), "tiles": tiles,
+                "cycles_per_tile": F16_TILE_CYCLES,
+                "basis": f"{F16_TILE_VALU} VALU x 4 cycles + {F16_TILE_TRANS} v_exp_f32 x 8 cycles per 32x32 wave-tile, "
+                         f"{SIMDS} SIMDs at {CLOCK_GHZ} GHz; FP16 MFMAs co-issue"}
     out["workload"] = (f"generic forward: B{batch} x H{heads} x L{length} x d{width}, radius {radius}, not causal "
                        f"(the generic entry point has no causal flag), {pairs} visited pairs")
     return out

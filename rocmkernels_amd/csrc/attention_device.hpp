@@ -127,6 +127,11 @@ __device__ __forceinline__ int buffer_load_byte(const Buffer r, const uint32_t v
     return __builtin_amdgcn_raw_buffer_load_b8(r, static_cast<int>(voffset), 0, 0);
 }
 
+// The byte at voffset + soffset (soffset scalar).
+__device__ __forceinline__ int buffer_load_byte_s(const Buffer r, const uint32_t voffset, const uint32_t soffset) {
+    return __builtin_amdgcn_raw_buffer_load_b8(r, static_cast<int>(voffset), static_cast<int>(soffset), 0);
+}
+
 // N contiguous floats at byte offset voffset (16-byte aligned when VEC).
 template<bool VEC, int N>
 __device__ __forceinline__ void buffer_load_span(float (&r)[N], const Buffer b, const uint32_t voffset) {

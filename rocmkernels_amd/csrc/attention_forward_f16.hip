@@ -64,13 +64,13 @@ constexpr int kVStride = D;
 // Operand of Oᵀ MFMA (t2, u) from the staged tile: lane (col, h) gets V[tile_row(8u + j, h)][32 t2 + col], j = 0..7,
 // as two transposing reads of 4 rows each. In each 16-lane group, lane L points at row r0 + L / 4, features
 // f0 + 4 (L mod 4) .. +3, and receives feature f0 + L of rows r0 .. r0 + 3 (r0 = 16u + 8p + 4h, f0 = 32 t2 + 16 (col / 16)).
-template<int D, int T2, int U>
+template<int D, int T2, int U, int STRIDE = kVStride<D>>
 __device__ __forceinline__ f16x8 read_v_operand(const _Float16 *slot, const int lane_off) {
     typedef __fp16 v4h __attribute__((ext_vector_type(4))); // the builtin's element type
-    const _Float16 *p = slot + lane_off + 16 * U * kVStride<D> + 32 * T2;
+    const _Float16 *p = slot + lane_off + 16 * U * STRIDE + 32 * T2;
     const f16x4 lo = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) v4h *)(p)));
     const f16x4 hi = __builtin_bit_cast(f16x4,
-            __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) v4h *)(p + 8 * kVStride<D>)));
+            __builtin_amdgcn_ds_read_tr16_b64_v4f16((__attribute__((address_space(3))) v4h *)(p + 8 * STRIDE)));
     return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
@@ -151,18 +151,30 @@ __global__ __launch_bounds__(kThreads) void attention_forward_f16_kernel(const T
     const int vrow = lane / VCPR; // row of the lane's chunk within each group of VRPL rows
     const int vwrite = vrow * kVStride<D> + 8 * (lane % VCPR);
     const int vread = (4 * h + ((lane & 15) >> 2)) * kVStride<D> + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    // With 128-bit rows the lane's offset within a tile is fixed (voffset) and the tile's row offset is scalar
+    // (soffset): no per-tile address arithmetic in the VALU.
+    const uint32_t kk_lane = static_cast<uint32_t>(col) * kstep + 16u * static_cast<uint32_t>(h);
+    const uint32_t vv_lane = static_cast<uint32_t>(vrow) * vstep + 16u * static_cast<uint32_t>(lane % VCPR);
     auto load_tile = [&](Tile &t, const int key0) __attribute__((always_inline)) {
         const uint32_t key = static_cast<uint32_t>(key0 + col);
-        t.mask = buffer_load_byte(mbuf, key);
+        if constexpr (VEC) {
+            const uint32_t k0 = static_cast<uint32_t>(key0);
+            t.mask = buffer_load_byte_s(mbuf, static_cast<uint32_t>(col), k0);
 #pragma unroll
-        for (int i = 0; i < KC; ++i) t.k[i] = load8h<VEC>(kbuf, key * kstep + 2u * (16 * i + 8 * h));
+            for (int i = 0; i < KC; ++i)
+                t.k[i] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(kbuf, static_cast<int>(kk_lane + 32u * i),
+                        static_cast<int>(k0 * kstep), 0));
+        } else {
+            t.mask = buffer_load_byte(mbuf, key);
+#pragma unroll
+            for (int i = 0; i < KC; ++i) t.k[i] = load8h<VEC>(kbuf, key * kstep + 2u * (16 * i + 8 * h));
+        }
         if constexpr (STAGE_V) {
-            // Rows past the sequence read 0 through the range check.
-            const uint32_t chunk = 16u * static_cast<uint32_t>(lane % VCPR);
+            // Rows past the sequence read 0 through the range check (which covers voffset + soffset).
 #pragma unroll
             for (int i = 0; i < VLOADS; ++i) {
-                const uint32_t row = static_cast<uint32_t>(key0 + VRPL * i + vrow);
-                t.vraw[i] = __builtin_amdgcn_raw_buffer_load_b128(vbuf, static_cast<int>(row * vstep + chunk), 0, 0);
+                t.vraw[i] = __builtin_amdgcn_raw_buffer_load_b128(vbuf, static_cast<int>(vv_lane + static_cast<uint32_t>(VRPL * i) * vstep),
+                        static_cast<int>(static_cast<uint32_t>(key0) * vstep), 0);
             }
         } else {
             // V[key0 + tile_row(8u + j, h)][32 t2 + col]; lanes past a 16-wide head's last feature read 0.
@@ -186,12 +198,13 @@ __global__ __launch_bounds__(kThreads) void attention_forward_f16_kernel(const T
         wave_lds_sync();
 #pragma unroll
         for (int i = 0; i < VLOADS; ++i) {
-            u32x4 x = t.vraw[i];
-            if (bits != 0xffffffffu) {
+            if (__builtin_expect(bits == 0xffffffffu, 1)) {
+                *reinterpret_cast<u32x4 *>(vslot + vwrite + VRPL * i * kVStride<D>) = t.vraw[i];
+            } else {
                 const bool kept = (bits >> (VRPL * i + vrow)) & 1u;
-                x = kept ? x : u32x4{0u, 0u, 0u, 0u};
+                __asm__ volatile("" ::: "memory"); // keeps the two stores apart (no select on the common path)
+                *reinterpret_cast<u32x4 *>(vslot + vwrite + VRPL * i * kVStride<D>) = kept ? t.vraw[i] : u32x4{0u, 0u, 0u, 0u};
             }
-            *reinterpret_cast<u32x4 *>(vslot + vwrite + VRPL * i * kVStride<D>) = x;
         }
     };
 
@@ -391,11 +404,12 @@ __global__ __launch_bounds__(kWave * QB * KS) __attribute__((amdgpu_waves_per_eu
     constexpr int KC = D / 16;                  // MFMAs per Sᵀ tile
     constexpr int DT = D / 32;                  // 32-feature output slices
     constexpr int KSTR = D + 8;                 // K stage row stride (halves): 16 bytes of padding, conflict-free row reads
+    constexpr int VSTR = D + 8;                 // V stage row stride: the four rows of a transposing read on distinct banks
     constexpr int CPR = D / 8;                  // 16-byte chunks per row
     constexpr int WCH = kTile * CPR / QB;       // chunks of a tile (K or V) loaded by one wave
     constexpr int NLOAD = (WCH + kWave - 1) / kWave;
     constexpr int ACTIVE = WCH < kWave ? WCH : kWave; // lanes that load
-    constexpr int KHALVES = kTile * KSTR, VHALVES = kTile * kVStride<D>;
+    constexpr int KHALVES = kTile * KSTR, VHALVES = kTile * VSTR;
     constexpr int STAGE_BYTES = 2 * KS * (KHALVES + VHALVES) * 2;
     constexpr int NREG = 16 * DT + 3;           // merged per lane: m, l, mc and the output accumulators
     constexpr int MERGE_BYTES = KS > 1 ? QB * NREG * kWave * 4 : 0;
@@ -464,34 +478,43 @@ __global__ __launch_bounds__(kWave * QB * KS) __attribute__((amdgpu_waves_per_eu
     };
     auto chunk_row = [&](const int i) { return (qi * WCH + kWave * i + lane) / CPR; };
     auto chunk_col = [&](const int i) { return (qi * WCH + kWave * i + lane) % CPR; };
-    // The loads of this stream's step i. Every step issues them unconditionally (a tile past the last one reads 0
-    // through the range check, offset kNoRow), so the loop has no branch around them.
+    // The loads of this stream's step i. Every step issues them unconditionally, so the loop has no branch around
+    // them: the lane's offset within a tile is fixed (voffset), the tile's row offset is scalar (soffset), and a tile
+    // past the last one gets soffset kNoRow, read as 0 by the range check (which covers voffset + soffset).
+    const uint32_t kv_lane = loader ? static_cast<uint32_t>(chunk_row(0)) * kstep + 16u * static_cast<uint32_t>(chunk_col(0)) : kNoRow;
+    const uint32_t vv_lane = loader ? static_cast<uint32_t>(chunk_row(0)) * vstep + 16u * static_cast<uint32_t>(chunk_col(0)) : kNoRow;
     auto issue = [&](Set &st, const int i) __attribute__((always_inline)) {
         const int t = i * KS + stream;
         const bool live = t < ntiles;
-        const int key0 = ufirst + t * kTile;
-        st.mbyte = buffer_load_byte(mbuf, live ? static_cast<uint32_t>(key0 + col) : kNoRow); // keys past the end read 0
+        const uint32_t key0 = static_cast<uint32_t>(ufirst + t * kTile);
+        st.mbyte = buffer_load_byte_s(mbuf, static_cast<uint32_t>(col), live ? key0 : kNoRow); // keys past the end read 0
 #pragma unroll
         for (int j = 0; j < NLOAD; ++j) {
-            const uint32_t row = static_cast<uint32_t>(key0 + chunk_row(j));
-            const uint32_t c16 = 16u * static_cast<uint32_t>(chunk_col(j));
-            const bool on = live && loader;
-            st.k[j] = __builtin_amdgcn_raw_buffer_load_b128(kbuf, static_cast<int>(on ? row * kstep + c16 : kNoRow), 0, 0);
-            st.v[j] = __builtin_amdgcn_raw_buffer_load_b128(vbuf, static_cast<int>(on ? row * vstep + c16 : kNoRow), 0, 0);
+            const uint32_t rows = static_cast<uint32_t>(kWave * j / CPR); // row offset of load j from load 0
+            st.k[j] = __builtin_amdgcn_raw_buffer_load_b128(kbuf, static_cast<int>(kv_lane), static_cast<int>(live ? (key0 + rows) * kstep : kNoRow), 0);
+            st.v[j] = __builtin_amdgcn_raw_buffer_load_b128(vbuf, static_cast<int>(vv_lane), static_cast<int>(live ? (key0 + rows) * vstep : kNoRow), 0);
         }
     };
-    // Writes a loaded tile into this stream's stage p; returns the tile's key-mask ballot.
+    // Writes a loaded tile into this stream's stage p; returns the tile's key-mask ballot. V rows of masked keys are
+    // written as zeros (only tiles with a masked key take that path).
+    const int kw_lane = chunk_row(0) * KSTR + 8 * chunk_col(0);
+    const int vw_lane = chunk_row(0) * VSTR + 8 * chunk_col(0);
     auto commit = [&](const Set &st, const int p) __attribute__((always_inline)) {
         const uint32_t bits = static_cast<uint32_t>(__ballot(st.mbyte != 0));
         if (loader) {
-            _Float16 *const ks = kstage(stream, p);
-            _Float16 *const vs = vstage(stream, p);
+            _Float16 *const ks = kstage(stream, p) + kw_lane;
+            _Float16 *const vs = vstage(stream, p) + vw_lane;
 #pragma unroll
             for (int j = 0; j < NLOAD; ++j) {
-                const int r = chunk_row(j), c = chunk_col(j);
-                const bool kept = (bits >> r) & 1u;
-                *reinterpret_cast<u32x4 *>(ks + r * KSTR + 8 * c) = st.k[j];
-                *reinterpret_cast<u32x4 *>(vs + r * kVStride<D> + 8 * c) = kept ? st.v[j] : u32x4{0u, 0u, 0u, 0u};
+                constexpr int ROWS = kWave / CPR; // rows between consecutive loads of a lane
+                *reinterpret_cast<u32x4 *>(ks + j * ROWS * KSTR) = st.k[j];
+                if (__builtin_expect(bits == 0xffffffffu, 1)) {
+                    *reinterpret_cast<u32x4 *>(vs + j * ROWS * VSTR) = st.v[j];
+                } else {
+                    const bool kept = (bits >> chunk_row(j)) & 1u;
+                    __asm__ volatile("" ::: "memory"); // keeps the two stores apart (no select on the common path)
+                    *reinterpret_cast<u32x4 *>(vs + j * ROWS * VSTR) = kept ? st.v[j] : u32x4{0u, 0u, 0u, 0u};
+                }
             }
         }
         return bits;
@@ -503,7 +526,7 @@ __global__ __launch_bounds__(kWave * QB * KS) __attribute__((amdgpu_waves_per_eu
     f32x16 o[DT];
 #pragma unroll
     for (int t = 0; t < DT; ++t) o[t] = f32x16{};
-    const int vread = (4 * h + ((lane & 15) >> 2)) * kVStride<D> + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    const int vread = (4 * h + ((lane & 15) >> 2)) * VSTR + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
     // The product of the tile at key0 from this stream's stage p for this wave's query tile.
     auto compute = [&](const int p, const int key0, const uint32_t bits) __attribute__((always_inline)) {
@@ -517,11 +540,11 @@ __global__ __launch_bounds__(kWave * QB * KS) __attribute__((amdgpu_waves_per_eu
         // covers the reads' LDS latency.
         __builtin_amdgcn_sched_barrier(0);
         f16x8 vop[DT][2];
-        vop[0][0] = read_v_operand<D, 0, 0>(vs, vread);
-        vop[0][1] = read_v_operand<D, 0, 1>(vs, vread);
+        vop[0][0] = read_v_operand<D, 0, 0, VSTR>(vs, vread);
+        vop[0][1] = read_v_operand<D, 0, 1, VSTR>(vs, vread);
         if constexpr (DT > 1) {
-            vop[DT - 1][0] = read_v_operand<D, DT - 1, 0>(vs, vread);
-            vop[DT - 1][1] = read_v_operand<D, DT - 1, 1>(vs, vread);
+            vop[DT - 1][0] = read_v_operand<D, DT - 1, 0, VSTR>(vs, vread);
+            vop[DT - 1][1] = read_v_operand<D, DT - 1, 1, VSTR>(vs, vread);
         }
         if (bits != 0xffffffffu || !tile_in_window(s, q0, key0)) {
             const uint32_t visible = (bits & bit_range(wlo - key0, whi - key0)) >> (4 * h);
@@ -563,18 +586,23 @@ __global__ __launch_bounds__(kWave * QB * KS) __attribute__((amdgpu_waves_per_eu
     // step before. A step: barrier (stage i mod 2 is complete; every wave is done reading the other stage), step i + 1's
     // tile from the registers into the other stage and step i + 2's loads into the registers, then step i's product:
     // the loads have a whole step (the product and the barrier) to land.
+    // The loop runs the steps in pairs (stages 0 and 1 at fixed offsets; an odd count gets one empty step).
     if (nsteps > 0) {
         Set st;
         issue(st, 0);
         uint32_t bits = commit(st, 0);
         issue(st, 1);
-        for (int i = 0; i < nsteps; ++i) {
+        auto step = [&](const int i, const int p) __attribute__((always_inline)) {
             __syncthreads();
-            const uint32_t next_bits = commit(st, (i + 1) & 1);
+            const uint32_t next_bits = commit(st, p ^ 1);
             issue(st, i + 2);
             const int t = i * KS + stream;
-            if (t < ntiles) compute(i & 1, ufirst + t * kTile, bits);
+            if (t < ntiles) compute(p, ufirst + t * kTile, bits);
             bits = next_bits;
+        };
+        for (int i = 0; i < nsteps; i += 2) {
+            step(i, 0);
+            step(i + 1, 1);
         }
     }
 
