@@ -284,12 +284,17 @@ __global__ __launch_bounds__(kWave * kBlockTiles * STREAMS) void attention_fused
                 f32x4 a[8];
 #pragma unroll
                 for (int u = 0; u < 8; ++u) a[u] = *reinterpret_cast<const f32x4 *>(arow + 4 * u);
-                f32x4 acc{0.0f, 0.0f, 0.0f, 0.0f};
+                // Two accumulator chains (even and odd 4-key groups), added at the end.
+                f32x4 acc{0.0f, 0.0f, 0.0f, 0.0f}, acc1{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-                for (int u = 0; u < 8; ++u) {
+                for (int u = 0; u < 8; u += 2) {
 #pragma unroll
-                    for (int x = 0; x < 4; ++x) acc = mfma16(a[u][x], kq[4 * u + x], acc);
+                    for (int x = 0; x < 4; ++x) {
+                        acc = mfma16(a[u][x], kq[4 * u + x], acc);
+                        acc1 = mfma16(a[u + 1][x], kq[4 * u + 4 + x], acc1);
+                    }
                 }
+                acc += acc1;
                 // Register x of lane l: query q0 + 16 rh + 4 (l / 16) + x, feature 16 fg + l % 16. Rows past the last
                 // query fall outside the resource and are dropped.
                 const uint32_t voff = (static_cast<uint32_t>(q0 + 16 * rh + 4 * (lane >> 4)) * D + 16u * fg + (lane & 15)) * 4u;
@@ -326,16 +331,15 @@ __global__ __launch_bounds__(kWave * kBlockTiles * STREAMS) void attention_fused
                         }
                     }
                     {
-                        float qr[HALF];
+                        // The S and dP chains are independent: interleaved, two accumulator chains are in flight.
+                        float qr[HALF], ur[HALF];
                         read_row_layout<D>(qslot, qr);
-#pragma unroll
-                        for (int c = 0; c < HALF; ++c) sc = mfma(qr[c], kr[c], sc);
-                    }
-                    {
-                        float ur[HALF];
                         read_row_layout<D>(uslot, ur);
 #pragma unroll
-                        for (int c = 0; c < HALF; ++c) dp = mfma(ur[c], vr[c], dp);
+                        for (int c = 0; c < HALF; ++c) {
+                            sc = mfma(qr[c], kr[c], sc);
+                            dp = mfma(ur[c], vr[c], dp);
+                        }
                     }
 #pragma unroll
                     for (int j = 0; j < 16; ++j) {
@@ -356,22 +360,26 @@ __global__ __launch_bounds__(kWave * kBlockTiles * STREAMS) void attention_fused
                     for (int j = 0; j < 16; ++j) dsp[tile_row(j, h) * kDsStride + 32 * w + col] = dp[j];
                     // dVᵀ += dOᵀ·P and dKᵀ += Qᵀ·dS: A operand of MFMA j is element [tile_row(j, h)][32t + col] of the
                     // tile, four consecutive j per 128-bit read of the feature-major copy.
-                    auto column_product = [&](const float *slot_t, const f32x16 &bop, f32x16 (&acc)[DT]) __attribute__((always_inline)) {
+                    // dVᵀ and dKᵀ interleaved (independent accumulator chains).
+                    const float *ut_slot = sh.ut[stream][p];
+                    const float *qt_slot = sh.qt[stream][p];
 #pragma unroll
-                        for (int u = 0; u < 4; ++u) {
-                            f32x4 c[DT];
+                    for (int u = 0; u < 4; ++u) {
+                        f32x4 cv[DT], ck[DT];
 #pragma unroll
-                            for (int t2 = 0; t2 < DT; ++t2)
-                                c[t2] = *reinterpret_cast<const f32x4 *>(slot_t + (32 * t2 + col) * kTStride + 8 * u + 4 * h);
+                        for (int t2 = 0; t2 < DT; ++t2) {
+                            cv[t2] = *reinterpret_cast<const f32x4 *>(ut_slot + (32 * t2 + col) * kTStride + 8 * u + 4 * h);
+                            ck[t2] = *reinterpret_cast<const f32x4 *>(qt_slot + (32 * t2 + col) * kTStride + 8 * u + 4 * h);
+                        }
 #pragma unroll
-                            for (int x = 0; x < 4; ++x) {
+                        for (int x = 0; x < 4; ++x) {
 #pragma unroll
-                                for (int t2 = 0; t2 < DT; ++t2) acc[t2] = mfma(c[t2][x], bop[4 * u + x], acc[t2]);
+                            for (int t2 = 0; t2 < DT; ++t2) {
+                                acc_v[t2] = mfma(cv[t2][x], sc[4 * u + x], acc_v[t2]);
+                                acc_k[t2] = mfma(ck[t2][x], dp[4 * u + x], acc_k[t2]);
                             }
                         }
-                    };
-                    column_product(sh.ut[stream][p], sc, acc_v);
-                    column_product(sh.qt[stream][p], dp, acc_k);
+                    }
                 } else {
 #pragma unroll
                     for (int j = 0; j < 16; ++j) dsp[tile_row(j, h) * kDsStride + 32 * w + col] = 0.0f;
