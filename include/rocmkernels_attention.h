@@ -33,10 +33,11 @@
  *   - deterministic: the reference's arrangement, a query-major dQ kernel and a key-major dK/dV kernel (7 matrix
  *     products per tile, S and dP computed in both); bit-identical results run to run.
  *   With neither bit 1 nor bit 2 set the library takes the faster one for the call: fused for inputs with 128-bit
- *   access (16-byte aligned pointers, strides multiples of 4), the band kernel under a radius window; deterministic
- *   otherwise. Bit 1 (ROCMKERNELS_ATTENTION_FUSED_BACKWARD) asks for fused wherever it exists (inputs
- *   with 128-bit access); bit 2 (ROCMKERNELS_ATTENTION_DETERMINISTIC) asks for deterministic. Setting both, or any
- *   other bit, returns hipErrorInvalidValue.
+ *   access (16-byte aligned pointers, strides multiples of 4), under a radius window the band kernel when there are at
+ *   least 5/8 as many 128-key blocks (batch x heads x ceil(keys / 128)) as compute units; deterministic otherwise.
+ *   Bit 1 (ROCMKERNELS_ATTENTION_FUSED_BACKWARD) asks for fused wherever it exists (inputs with 128-bit access); bit 2
+ *   (ROCMKERNELS_ATTENTION_DETERMINISTIC) asks for deterministic. Setting both, or any other bit, returns
+ *   hipErrorInvalidValue.
  * The reference-named backward entry points always run the deterministic kernels, as the reference's do.
  */
 #ifndef ROCMKERNELS_ATTENTION_H
