@@ -197,7 +197,10 @@ def measure_rotary(cfg, steps, warmup):
     (RotaryBenchmarks.cpp:52-53): HBM-bound, reported against the 8 TB/s HBM peak with the algorithmic bytes (Q, K
     read; oq, ok written; cos/sin tables read once). Consecutive launches cycle through enough copies of the inputs and
     outputs (ROTARY_COLD_MIB in all) that every launch reads its inputs from HBM, not from the Infinity Cache the
-    previous launch filled."""
+    previous launch filled: a sample replays a graph that launches every set in turn, R times (R such that the sample
+    lasts at least SAMPLE_MS), after a cache flush. Every set's outputs are then checked bit for bit against an eager
+    launch on set 0 (all sets hold the same inputs)."""
+    import numpy as np
     import torch
 
     from rocmkernels_amd import attention, inputs
@@ -216,19 +219,47 @@ def measure_rotary(cfg, steps, warmup):
         cos, sin = cos0.to(device), sin0.to(device)
         oq = torch.empty((batch, length, heads, 32), device=device)
         sets.append((q, k, cos, sin, oq, torch.empty_like(oq)))
-    turn = [0]
 
-    def launch():
-        q, k, cos, sin, oq, ok = sets[turn[0] % nsets]
-        turn[0] += 1
+    def launch(i):
+        q, k, cos, sin, oq, ok = sets[i]
         attention.rotary(q, k, cos, sin, out_q=oq, out_k=ok)
 
-    launch()
-    # Every set holds the same inputs, so the outputs of set 0 are checked after each replay.
-    ms = time_graph(launch, steps, list(sets[0][4:]))
+    launch(0)
+    torch.cuda.synchronize()
+    want = [t.clone() for t in sets[0][4:]]
+    stream = torch.cuda.current_stream()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(nsets):
+        launch(i)
+    stop.record(stream)
+    torch.cuda.synchronize()
+    reps = max(1, int(np.ceil(SAMPLE_MS / max(start.elapsed_time(stop), 1e-3))))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            for i in range(nsets):
+                launch(i)
+    settle(graph.replay, per_check=1)
+    times = []
+    for _ in range(max(steps, SAMPLES_MIN)):
+        flush_caches()
+        torch.cuda.synchronize()
+        start.record(stream)
+        graph.replay()
+        stop.record(stream)
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(stop) / (reps * nsets))
+    for st in sets:
+        for got, ref in zip(st[4:], want):
+            if not torch.equal(got.view(torch.int32), ref.view(torch.int32)):
+                raise RuntimeError("rotary: a replayed launch differs from the eager one")
+    ms = float(np.median(times))
     return {"ms_per_launch": round(ms, 6), "bytes_per_launch": nbytes, "gbps": round(nbytes / (ms * 1e-3) / 1e9, 2),
             "frac_of_hbm_peak": round(nbytes / (ms * 1e-3) / 8e12, 4), "shape": f"B{batch} H{heads} L{length} d32",
-            "inputs": f"{nsets} distinct input/output sets of {nbytes / 2**20:.1f} MiB cycled, so each launch reads HBM"}
+            "samples": len(times), "launches_per_sample": reps * nsets,
+            "inputs": f"{nsets} distinct input/output sets of {nbytes / 2**20:.1f} MiB launched in turn, so each launch reads HBM"}
 
 
 def cpu_threads():
