@@ -383,40 +383,44 @@ __global__ __launch_bounds__(kThreads) void attention_forward_f16_kernel(const T
     }
 }
 
-// Shared K/V tiles: QB query tiles of one sequence per workgroup (d = 64, 16-byte aligned rows, every stride a
-// multiple of 8). Wave w of the workgroup owns query tile QB·block + w mod QB and key stream w / QB: the KS streams
-// take alternate key tiles of the union of the workgroup's windows. The QB waves of a stream stream its tiles together:
-// each loads 1/QB of a tile's K and V rows (whole 128-byte lines) into the stream's double-buffered LDS stage, which all
-// of them read, so every K/V byte crosses from L2 once per QB waves instead of once per wave, and the loads run two
-// tiles ahead of their use. Per step: one workgroup barrier; then the next tile's rows go from registers into the
-// other stage (V rows of masked keys as zeros) and the loads of the tile after it are issued; then each wave whose
-// window meets the tile computes it as attention_forward_f16_kernel does (K's row layout read from the stage with
-// 128-bit LDS reads, V's operand with transposing reads). Every wave runs every step (the barriers are uniform); a wave
-// past the last query tile or outside the tile's window only loads and stores its share. With KS = 2 the second
-// stream's softmax state is merged into the first through LDS at the end (a fixed order: deterministic). The kernel
-// is held to 128 VGPRs, so four waves fit on every SIMD.
+// Shared K/V tiles: QB = 4 query tiles of one sequence per workgroup (d = 64, 16-byte aligned rows, every stride a
+// multiple of 8). Wave w of the workgroup owns query tile 4·block + w mod 4 and key stream w / 4: the KS streams take
+// alternate key tiles of the union of the workgroup's windows. The four waves of a stream stream its tiles together:
+// each loads a quarter of a tile's K and V rows (one 16-byte chunk per lane of each, whole 128-byte lines) straight into
+// the stream's double-buffered LDS stage (buffer loads with the LDS bit: no registers, no LDS store instructions), which
+// all of them read, so every K/V byte crosses from L2 once per four waves instead of once per wave. Per step: one
+// workgroup barrier (its fence waits for this wave's loads, so after it every wave's share of the tile is in place and
+// every wave is done reading the other stage); then the loads of the next tile into the other stage; then each wave
+// whose window meets the tile computes it as attention_forward_f16_kernel does (K's row layout read with 128-bit LDS
+// reads, V's operand with transposing reads; V elements of masked keys are zeroed in registers, only on tiles with a
+// masked key). Loads write 64 consecutive 16-byte chunks per instruction, so the stage rows are unpadded and the
+// chunks of each row are permuted (an XOR of the chunk index with a function of the row) to keep the reads free of
+// bank conflicts. Every wave runs every step (the barriers are uniform); a wave past the last query tile or outside the
+// tile's window only loads its share. With KS = 2 the second stream's softmax state is merged into the first through
+// LDS at the end (a fixed order: deterministic). The kernel is held to 128 VGPRs, so four waves fit on every SIMD.
 template<int D, int QB, int KS>
 __global__ __launch_bounds__(kWave * QB * KS) __attribute__((amdgpu_waves_per_eu(4))) void attention_forward_f16_shared_kernel(
         const TensorH q, const TensorH k, const TensorH v, const uint8_t *__restrict__ mask, _Float16 *__restrict__ out,
         const int osb, const int osh, const int ost, float *__restrict__ lse, const Shape s, const float scale) {
     static_assert(D == 64, "shared K/V tiles are for 64-wide heads (at d = 32 the per-wave kernel is faster)");
-    static_assert((QB == 2 || QB == 4) && (KS == 1 || KS == 2));
+    static_assert(QB == 4 && (KS == 1 || KS == 2));
     constexpr int KC = D / 16;                  // MFMAs per Sᵀ tile
     constexpr int DT = D / 32;                  // 32-feature output slices
-    constexpr int KSTR = D + 8;                 // K stage row stride (halves): 16 bytes of padding, conflict-free row reads
-    constexpr int VSTR = D + 8;                 // V stage row stride: the four rows of a transposing read on distinct banks
     constexpr int CPR = D / 8;                  // 16-byte chunks per row
-    constexpr int WCH = kTile * CPR / QB;       // chunks of a tile (K or V) loaded by one wave
-    constexpr int NLOAD = (WCH + kWave - 1) / kWave;
-    constexpr int ACTIVE = WCH < kWave ? WCH : kWave; // lanes that load
-    constexpr int KHALVES = kTile * KSTR, VHALVES = kTile * VSTR;
-    constexpr int STAGE_BYTES = 2 * KS * (KHALVES + VHALVES) * 2;
+    static_assert(kTile * CPR == QB * kWave, "each wave of a stream loads one chunk per lane of a K tile and of a V tile");
+    constexpr int TILE = kTile * D;             // halves of one staged K or V tile (rows D halves apart)
+    constexpr int STAGE_BYTES = 2 * KS * 2 * TILE * 2;
     constexpr int NREG = 16 * DT + 3;           // merged per lane: m, l, mc and the output accumulators
     constexpr int MERGE_BYTES = KS > 1 ? QB * NREG * kWave * 4 : 0;
     __shared__ __align__(16) unsigned char smem[STAGE_BYTES > MERGE_BYTES ? STAGE_BYTES : MERGE_BYTES];
-    // Stage (stream x, parity p): K rows then V rows.
-    auto kstage = [&](const int x, const int p) { return reinterpret_cast<_Float16 *>(smem) + (2 * x + p) * (KHALVES + VHALVES); };
-    auto vstage = [&](const int x, const int p) { return kstage(x, p) + KHALVES; };
+    // Stage (stream x, parity p): the K tile, then the V tile.
+    auto kstage = [&](const int x, const int p) { return reinterpret_cast<_Float16 *>(smem) + (2 * x + p) * (2 * TILE); };
+    auto vstage = [&](const int x, const int p) { return kstage(x, p) + TILE; };
+    // Chunk c of row r is stored at position c ^ kswz(r) (K) or c ^ vswz(r) (V) of the row. K's row-layout reads (16
+    // lanes: 16 rows, one chunk each) then meet 16 distinct 16-byte bank groups, and V's transposing reads (16 lanes: 4
+    // rows of 32 bytes) 8; the V permutation leaves rows 4 apart alike, so a read 8 or 16 rows further is an offset.
+    auto kswz = [](const int r) { return (r & 7) ^ ((r >> 3) & 1); };
+    auto vswz = [](const int r) { return 2 * (r & 3); };
 
     const int lane = threadIdx.x & (kWave - 1);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
@@ -470,54 +474,25 @@ __global__ __launch_bounds__(kWave * QB * KS) __attribute__((amdgpu_waves_per_eu
     for (int i = 0; i < KC; ++i)
         qr[i] = load8h<true>(qbuf, tile_valid ? static_cast<uint32_t>(query) * (2u * q.st) + 2u * (16 * i + 8 * h) : kNoRow);
 
-    // This lane's chunks of its stream's tiles: chunk c = qi * WCH + 64 i + lane, row c / CPR, 16-byte column c mod CPR.
-    const bool loader = lane < ACTIVE;
-    struct Set {
-        u32x4 k[NLOAD], v[NLOAD];
-        int mbyte;
-    };
-    auto chunk_row = [&](const int i) { return (qi * WCH + kWave * i + lane) / CPR; };
-    auto chunk_col = [&](const int i) { return (qi * WCH + kWave * i + lane) % CPR; };
-    // The loads of this stream's step i. Every step issues them unconditionally, so the loop has no branch around
-    // them: the lane's offset within a tile is fixed (voffset), the tile's row offset is scalar (soffset), and a tile
-    // past the last one gets soffset kNoRow, read as 0 by the range check (which covers voffset + soffset).
-    const uint32_t kv_lane = loader ? static_cast<uint32_t>(chunk_row(0)) * kstep + 16u * static_cast<uint32_t>(chunk_col(0)) : kNoRow;
-    const uint32_t vv_lane = loader ? static_cast<uint32_t>(chunk_row(0)) * vstep + 16u * static_cast<uint32_t>(chunk_col(0)) : kNoRow;
-    auto issue = [&](Set &st, const int i) __attribute__((always_inline)) {
+    // This lane's load of a stream tile fills stage chunk 64·qi + lane: row lrow, position lane mod 8, i.e. the
+    // row's chunk (lane mod 8) ^ swz(lrow). Its offset within a tile is fixed (voffset); the tile's row offset is
+    // scalar (soffset), and a tile past the last one gets soffset kNoRow, read as 0 by the range check (which covers
+    // voffset + soffset), as are rows past the sequence's end.
+    const int lrow = (kWave * qi + lane) / CPR;
+    const uint32_t kv_lane = static_cast<uint32_t>(lrow) * kstep + 16u * static_cast<uint32_t>((lane & 7) ^ kswz(lrow));
+    const uint32_t vv_lane = static_cast<uint32_t>(lrow) * vstep + 16u * static_cast<uint32_t>((lane & 7) ^ vswz(lrow));
+    // Issues step i's loads into stage p: K and V rows into LDS, the tile's mask bytes (one per key, lane col) into the
+    // returned register.
+    auto issue = [&](const int i, const int p) __attribute__((always_inline)) {
         const int t = i * KS + stream;
         const bool live = t < ntiles;
         const uint32_t key0 = static_cast<uint32_t>(ufirst + t * kTile);
-        st.mbyte = buffer_load_byte_s(mbuf, static_cast<uint32_t>(col), live ? key0 : kNoRow); // keys past the end read 0
-#pragma unroll
-        for (int j = 0; j < NLOAD; ++j) {
-            const uint32_t rows = static_cast<uint32_t>(kWave * j / CPR); // row offset of load j from load 0
-            st.k[j] = __builtin_amdgcn_raw_buffer_load_b128(kbuf, static_cast<int>(kv_lane), static_cast<int>(live ? (key0 + rows) * kstep : kNoRow), 0);
-            st.v[j] = __builtin_amdgcn_raw_buffer_load_b128(vbuf, static_cast<int>(vv_lane), static_cast<int>(live ? (key0 + rows) * vstep : kNoRow), 0);
-        }
-    };
-    // Writes a loaded tile into this stream's stage p; returns the tile's key-mask ballot. V rows of masked keys are
-    // written as zeros (only tiles with a masked key take that path).
-    const int kw_lane = chunk_row(0) * KSTR + 8 * chunk_col(0);
-    const int vw_lane = chunk_row(0) * VSTR + 8 * chunk_col(0);
-    auto commit = [&](const Set &st, const int p) __attribute__((always_inline)) {
-        const uint32_t bits = static_cast<uint32_t>(__ballot(st.mbyte != 0));
-        if (loader) {
-            _Float16 *const ks = kstage(stream, p) + kw_lane;
-            _Float16 *const vs = vstage(stream, p) + vw_lane;
-#pragma unroll
-            for (int j = 0; j < NLOAD; ++j) {
-                constexpr int ROWS = kWave / CPR; // rows between consecutive loads of a lane
-                *reinterpret_cast<u32x4 *>(ks + j * ROWS * KSTR) = st.k[j];
-                if (__builtin_expect(bits == 0xffffffffu, 1)) {
-                    *reinterpret_cast<u32x4 *>(vs + j * ROWS * VSTR) = st.v[j];
-                } else {
-                    const bool kept = (bits >> chunk_row(j)) & 1u;
-                    __asm__ volatile("" ::: "memory"); // keeps the two stores apart (no select on the common path)
-                    *reinterpret_cast<u32x4 *>(vs + j * ROWS * VSTR) = kept ? st.v[j] : u32x4{0u, 0u, 0u, 0u};
-                }
-            }
-        }
-        return bits;
+        const int mbyte = buffer_load_byte_s(mbuf, static_cast<uint32_t>(col), live ? key0 : kNoRow); // keys past the end read 0
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(kbuf, (__attribute__((address_space(3))) void *)(kstage(stream, p) + kWave * 8 * qi), 16,
+                static_cast<int>(kv_lane), static_cast<int>(live ? key0 * kstep : kNoRow), 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(vbuf, (__attribute__((address_space(3))) void *)(vstage(stream, p) + kWave * 8 * qi), 16,
+                static_cast<int>(vv_lane), static_cast<int>(live ? key0 * vstep : kNoRow), 0, 0);
+        return mbyte;
     };
 
     constexpr float kLazy = 8.0f; // p = exp2(s·c2 - mc) <= 2^8: also within fp16 range
@@ -526,30 +501,61 @@ __global__ __launch_bounds__(kWave * QB * KS) __attribute__((amdgpu_waves_per_eu
     f32x16 o[DT];
 #pragma unroll
     for (int t = 0; t < DT; ++t) o[t] = f32x16{};
-    const int vread = (4 * h + ((lane & 15) >> 2)) * VSTR + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+    // Lane offsets (halves) of this lane's reads within a stage: K rows col, chunks 2i + h (row layout); V as the
+    // transposing reads of read_v_operand address them (16-lane group: rows 4h + (lane mod 16) / 4, features
+    // 32 t2 + 16 ((lane / 16) mod 2) + 4 (lane mod 4)), permuted as the loads stored them.
+    int kread[KC];
+#pragma unroll
+    for (int i = 0; i < KC; ++i) kread[i] = col * D + 8 * ((2 * i + h) ^ kswz(col));
+    int vread[DT];
+#pragma unroll
+    for (int t2 = 0; t2 < DT; ++t2) {
+        const int vrow = 4 * h + ((lane & 15) >> 2);
+        const int chunk = 4 * t2 + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+        vread[t2] = vrow * D + 8 * (chunk ^ vswz(vrow)) + 4 * (lane & 1);
+    }
 
-    // The product of the tile at key0 from this stream's stage p for this wave's query tile.
-    auto compute = [&](const int p, const int key0, const uint32_t bits) __attribute__((always_inline)) {
-        if (!tile_valid || bits == 0 || key0 >= last || key0 + kTile <= first) return;
-        const _Float16 *kp = kstage(stream, p) + col * KSTR + 8 * h;
+    // The MFMA operands of the tile in this stream's stage p: K's row layout (Sᵀ A operands) and V's transposed layout
+    // (Oᵀ A operands).
+    struct Operands {
+        f16x8 k[KC];
+        f16x8 v[DT][2];
+    };
+    auto read_operands = [&](Operands &op, const int p) __attribute__((always_inline)) {
+        const _Float16 *ks = kstage(stream, p);
         const _Float16 *vs = vstage(stream, p);
+#pragma unroll
+        for (int i = 0; i < KC; ++i) op.k[i] = *reinterpret_cast<const f16x8 *>(ks + kread[i]);
+#pragma unroll
+        for (int t2 = 0; t2 < DT; ++t2) {
+            op.v[t2][0] = read_v_operand<D, 0, 0, D>(vs, vread[t2]);
+            op.v[t2][1] = read_v_operand<D, 0, 1, D>(vs, vread[t2]);
+        }
+    };
+    // The product of the tile at key0 for this wave's query tile.
+    auto compute = [&](Operands &op, const int key0, const uint32_t bits) __attribute__((always_inline)) {
+        auto &vop = op.v;
         f32x16 sc{};
 #pragma unroll
-        for (int i = 0; i < KC; ++i) sc = mfma16(*reinterpret_cast<const f16x8 *>(kp + 16 * i), qr[i], sc);
-        // V's operands are read once the K operands are consumed (their registers are free again); the softmax below
-        // covers the reads' LDS latency.
-        __builtin_amdgcn_sched_barrier(0);
-        f16x8 vop[DT][2];
-        vop[0][0] = read_v_operand<D, 0, 0, VSTR>(vs, vread);
-        vop[0][1] = read_v_operand<D, 0, 1, VSTR>(vs, vread);
-        if constexpr (DT > 1) {
-            vop[DT - 1][0] = read_v_operand<D, DT - 1, 0, VSTR>(vs, vread);
-            vop[DT - 1][1] = read_v_operand<D, DT - 1, 1, VSTR>(vs, vread);
-        }
+        for (int i = 0; i < KC; ++i) sc = mfma16(op.k[i], qr[i], sc);
         if (bits != 0xffffffffu || !tile_in_window(s, q0, key0)) {
             const uint32_t visible = (bits & bit_range(wlo - key0, whi - key0)) >> (4 * h);
 #pragma unroll
             for (int j = 0; j < 16; ++j) sc[j] = (visible >> (8 * (j >> 2) + (j & 3))) & 1u ? sc[j] : -INFINITY;
+            if (bits != 0xffffffffu) {
+                // Masked keys contribute exactly nothing, whatever their stored V rows hold: element j of operand u
+                // is key 16u + 8 (j / 4) + 4h + j mod 4.
+                const uint32_t kept = bits >> (4 * h);
+#pragma unroll
+                for (int t2 = 0; t2 < DT; ++t2) {
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+                        for (int j = 0; j < 8; ++j)
+                            vop[t2][u][j] = (kept >> (16 * u + 8 * (j >> 2) + (j & 3))) & 1u ? vop[t2][u][j] : static_cast<_Float16>(0.0f);
+                    }
+                }
+            }
         }
         float mx = m_half;
 #pragma unroll
@@ -582,28 +588,34 @@ __global__ __launch_bounds__(kWave * QB * KS) __attribute__((amdgpu_waves_per_eu
         }
     };
 
-    // Step i of stream x: tile i·KS + x, loaded into the register set two steps before, written to stage i mod 2 one
-    // step before. A step: barrier (stage i mod 2 is complete; every wave is done reading the other stage), step i + 1's
-    // tile from the registers into the other stage and step i + 2's loads into the registers, then step i's product:
-    // the loads have a whole step (the product and the barrier) to land.
-    // The loop runs the steps in pairs (stages 0 and 1 at fixed offsets; an odd count gets one empty step).
+    // Step i of stream x: tile i·KS + x, loaded into stage i mod 2 during step i - 1. A step: barrier (its fence waits
+    // for this wave's outstanding loads: stage i mod 2 is complete, and every wave is done reading the other stage);
+    // the operands of step i's tile from the stage; step i + 1's loads into the other stage; then step i's product: the
+    // loads have the product and the barrier to land. The operand reads come before the loads are issued: the compiler
+    // makes an LDS read that follows an LDS-bound load wait for that load, whatever the addresses. The loop runs the
+    // steps in pairs (stages 0 and 1 at fixed offsets; an odd count gets one empty step).
     if (nsteps > 0) {
-        Set st;
-        issue(st, 0);
-        uint32_t bits = commit(st, 0);
-        issue(st, 1);
+        int mnext = issue(0, 0);
         auto step = [&](const int i, const int p) __attribute__((always_inline)) {
             __syncthreads();
-            const uint32_t next_bits = commit(st, p ^ 1);
-            issue(st, i + 2);
+            const uint32_t bits = static_cast<uint32_t>(__ballot(mnext != 0));
             const int t = i * KS + stream;
-            if (t < ntiles) compute(p, ufirst + t * kTile, bits);
-            bits = next_bits;
+            const int key0 = ufirst + t * kTile;
+            const bool work = t < ntiles && tile_valid && bits != 0 && key0 < last && key0 + kTile > first;
+            Operands op;
+            if (work) read_operands(op, p);
+            __builtin_amdgcn_sched_barrier(0);
+            mnext = issue(i + 1, p ^ 1);
+            __builtin_amdgcn_sched_barrier(0);
+            if (work) compute(op, key0, bits);
         };
         for (int i = 0; i < nsteps; i += 2) {
             step(i, 0);
             step(i + 1, 1);
         }
+        // The last step's loads (past the last tile: zeros) write LDS: they land before the stages are reused or the
+        // workgroup ends.
+        __syncthreads();
     }
 
     const float m_run = halves_max(m_half);
