@@ -52,10 +52,22 @@ __global__ __launch_bounds__(256) void rotary_kernel(const float *__restrict__ q
     const int64_t row = thread >> 2;
     if (row >= rows) return;
     const int part = 4 * static_cast<int>(thread & 3);
-    const int head = static_cast<int>(row % heads);
-    const int64_t sample_token = row / heads;
-    const int token = static_cast<int>(sample_token % length);
-    const int64_t sample = sample_token / length;
+    // Head, token and sample of the row; 32-bit divisions whenever the rows fit (64-bit ones are long VALU sequences).
+    int head, token;
+    int64_t sample;
+    if (rows <= 0xffffffffLL) {
+        const uint32_t r32 = static_cast<uint32_t>(row), nh = static_cast<uint32_t>(heads), nl = static_cast<uint32_t>(length);
+        const uint32_t sample_token = r32 / nh;
+        head = static_cast<int>(r32 - sample_token * nh);
+        const uint32_t s32 = sample_token / nl;
+        token = static_cast<int>(sample_token - s32 * nl);
+        sample = s32;
+    } else {
+        head = static_cast<int>(row % heads);
+        const int64_t sample_token = row / heads;
+        token = static_cast<int>(sample_token % length);
+        sample = sample_token / length;
+    }
 
     const float *qrow = q + sample * qs.batch + static_cast<int64_t>(head) * qs.head + static_cast<int64_t>(token) * qs.token + part;
     const float *krow = k + sample * ks.batch + static_cast<int64_t>(head) * ks.head + static_cast<int64_t>(token) * ks.token + part;
