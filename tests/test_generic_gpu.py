@@ -269,8 +269,8 @@ def test_generic_fp16_shared_kv_tiles(device, width, batch, heads, queries, keys
 
 @pytest.mark.parametrize("width", [32, 64])
 def test_generic_fp16_shared_kv_tiles_garbage_and_masked_batch(device, width):
-    # Masked keys holding inf (K) and NaN (V) contribute nothing through the shared stages (their V rows are written
-    # as zeros, their scores dropped), and a fully masked batch gives O = 0, lse = {-inf, 0}.
+    # Masked keys holding inf (K) and NaN (V) contribute nothing through the shared stages (their V elements are zeroed
+    # in the operand registers, their scores dropped), and a fully masked batch gives O = 0, lse = {-inf, 0}.
     batch, heads, queries, keys = 32, 8, 96, 100
     q, k, v = (inputs.normal(1100 + i, (batch, heads, n, width)).astype(np.float16) for i, n in enumerate((queries, keys, keys)))
     mask = np.ones((batch, keys), np.uint8)
@@ -285,3 +285,27 @@ def test_generic_fp16_shared_kv_tiles_garbage_and_masked_batch(device, width):
     out, lse = run(device, q, k, v, mask)
     check(out, lse, want, "f16", f"d{width} shared, garbage in masked rows")
     assert np.all(out[2] == 0.0) and np.all(lse[2, ..., 0] == -np.inf) and np.all(lse[2, ..., 1] == 0.0)
+
+
+@pytest.mark.parametrize("case", range(12))
+def test_generic_fp16_shared_kv_tiles_random_shapes(device, case):
+    # Seeded random shapes on the shared K/V kernel (d = 64, at least one workgroup of four query tiles per CU): query
+    # and key counts that leave partial tiles and partial workgroups, radius windows, key padding; both stream counts.
+    rng = np.random.default_rng(7000 + case)
+    seqs = int(rng.choice([256, 320, 512, 1024]))
+    heads = int(rng.choice([1, 2, 4, 8]))
+    batch = seqs // heads
+    queries = int(rng.integers(1, 3)) * 128 - int(rng.integers(0, 100))
+    keys = int(rng.integers(1, 300))
+    radius = -1 if rng.random() < 0.4 else int(rng.integers(0, 160))
+    seed = 7100 + 10 * case
+    q = inputs.normal(seed, (batch, heads, queries, 64)).astype(np.float16)
+    k = inputs.normal(seed + 1, (batch, heads, keys, 64)).astype(np.float16)
+    v = inputs.normal(seed + 2, (batch, heads, keys, 64)).astype(np.float16)
+    mask = np.ones((batch, keys), np.uint8)
+    if rng.random() < 0.6:
+        lengths = inputs.uniform_int(seed + 3, batch, 1, keys)
+        mask = (np.arange(keys)[None, :] < lengths[:, None]).astype(np.uint8)
+    want = oracle.attention(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32), mask, radius=radius)
+    out, lse = run(device, q, k, v, mask, radius=radius)
+    check(out, lse, want, "f16", f"case {case}: {batch}x{heads} {queries}x{keys} d64 r{radius} shared")
