@@ -309,3 +309,20 @@ def test_generic_fp16_shared_kv_tiles_random_shapes(device, case):
     want = oracle.attention(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32), mask, radius=radius)
     out, lse = run(device, q, k, v, mask, radius=radius)
     check(out, lse, want, "f16", f"case {case}: {batch}x{heads} {queries}x{keys} d64 r{radius} shared")
+
+
+@pytest.mark.parametrize("radius", [-1, 20])
+def test_generic_fp16_shared_kv_tiles_token_major(device, radius):
+    # [B][T][H][D] storage viewed as [B][H][T][D] on the shared K/V kernel (256 sequences): the stage loads step by the
+    # token stride H*D, not the head width.
+    batch, heads, queries, keys, width = 64, 4, 100, 90, 64
+    arrays = [inputs.normal(7300 + i, (batch, n, heads, width)).astype(np.float16) for i, n in enumerate((queries, keys, keys))]
+    views = [torch.from_numpy(a).to(device).permute(0, 2, 1, 3) for a in arrays]
+    assert views[1].stride(2) == heads * width
+    mask = np.ones((batch, keys), np.uint8)
+    mask[3, 70:] = 0
+    mask[5, :10] = 0
+    out, lse = attention.generic_forward(*views, torch.from_numpy(mask).to(device), radius=radius)
+    torch.cuda.synchronize()
+    want = oracle.attention(*(a.transpose(0, 2, 1, 3).astype(np.float32) for a in arrays), mask, radius=radius)
+    check(out.float().cpu().numpy(), lse.cpu().numpy(), want, "f16", f"d64 token-major shared r{radius}")
