@@ -17,7 +17,8 @@
 //     the merge of the waves sharing a query tile follow attention_forward.hip.
 //   * Two kernels: attention_forward_f16_kernel gives each wave its own K/V tiles (1, 2 or 4 waves per query tile);
 //     at d = 64 on grids that fill the chip, attention_forward_f16_shared_kernel has the waves of a workgroup (four query
-//     tiles of one sequence) share each K/V tile through LDS, a quarter of the per-wave kernel's L2 traffic.
+//     tiles of one sequence) share each K/V tile through LDS, a quarter of the per-wave kernel's L2 traffic; its tiles
+//     are loaded straight into LDS (buffer loads with the LDS bit).
 #include "attention_device.hpp"
 #include "attention_launch.hpp"
 
